@@ -1,0 +1,103 @@
+/*
+ * tensorvia_hip.h — C-ABI of the MI355X (gfx950) HIP matmul backend.
+ *
+ * This is the boundary between Tensorvia's C++ op layer and the hand-written HIP kernels.
+ * It carries plain pointers, sizes and element strides only: no C++ types, no exceptions,
+ * no tensor allocation.  Every entry point returns 0 on success, a positive hipError_t value
+ * when the HIP runtime failed, or a negative TV_E_* code when the arguments were rejected.
+ *
+ * Reference interfaces replaced (paths into Aimol-l/Tensorvia):
+ *   tv_hip_gemm   <- template<> struct MulImpl<Device::CUDA> { static Tensor execute(a, b); }
+ *                    (include/backend/cuda/ops/mul.h:6-15, src/backend/cuda/mul.cu:52-124) and its
+ *                    kernel launch mul_cuda_3d<<<...>>> (src/backend/cuda/mul.cu:8-48,77-91).
+ *                    The descriptor also covers the view metadata that ops::Mul receives through
+ *                    Tensor (Metadata, include/core/tensor.h:12-27) so strided and broadcast
+ *                    operands are consumed without a repack.
+ *   tv_hip_gemv   <- the batch*M*N < 2^20 "basic" branch of mul_kernel (src/backend/cpu/mul.cpp:7-25,
+ *                    87-96) that decode-shaped calls (M <= 8) take; no CUDA counterpart exists.
+ *   tv_hip_strerror <- the std::runtime_error texts the reference throws (src/ops.cpp:542-556,
+ *                    include/backend/cuda/cuda_tensor.cpp:20-23).
+ *
+ * Semantics (matching the reference CPU backend, src/backend/cpu/mul.cpp:97-145):
+ *   C[b, m, n] = sum_k A[b, m, k] * B[b, k, n]
+ *   - element (b, m, k) of A lives at  A + b*sa_b + m*sa_m + k*sa_k  (element units);
+ *     sa_b == 0 broadcasts A over the batch, likewise sb_b for B;
+ *   - int8 x int8: exact int32 accumulation; dtype_c INT8 stores the low byte of the exact sum
+ *     (the reference's wrap-around result), dtype_c INT32 stores the full sum;
+ *   - bf16/fp16 inputs: fp32 accumulation, output bf16/fp16 (GPU-backend convention) or FLOAT32
+ *     (the CPU backend's widened result);
+ *   - fp32: fp32 accumulation on the fp32 matrix cores;
+ *   - any other dtype pair: exact restatement of the reference CPU accumulation rules on a
+ *     SIMT kernel (slow path, provided for completeness).
+ *
+ * Calls are asynchronous on `hip_stream` (a hipStream_t, NULL = default stream).  The caller
+ * keeps A, B and C alive until the stream has executed the work.  Calls that overlap on one
+ * device share the library's GEMV reduction workspace only through per-call regions, so
+ * concurrent streams are safe.
+ */
+#ifndef TENSORVIA_HIP_H
+#define TENSORVIA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* via::DataType values (reference include/core/type_traits.h:123-132). */
+enum tv_dtype {
+    TV_INT8 = 0,
+    TV_INT16 = 1,
+    TV_INT32 = 2,
+    TV_INT64 = 3,
+    TV_BFLOAT16 = 4,
+    TV_FLOAT16 = 5,
+    TV_FLOAT32 = 6,
+    TV_FLOAT64 = 7
+};
+
+/* Negative error codes; positive codes are hipError_t values. */
+enum tv_status {
+    TV_OK = 0,
+    TV_E_NULL = -1,        /* a required pointer is NULL */
+    TV_E_SHAPE = -2,       /* batch/M/N/K negative or a size overflows the kernels' index range */
+    TV_E_DTYPE = -3,       /* dtype value out of range or output dtype not allowed for the inputs */
+    TV_E_UNSUPPORTED = -4, /* valid request that this entry point does not serve (e.g. gemv with M > 8) */
+    TV_E_INJECTED = -5,    /* returned by the fault-injection hook (tests only) */
+    TV_E_NOMEM = -6        /* workspace allocation failed */
+};
+
+typedef struct tv_gemm_args {
+    int32_t dtype_a, dtype_b, dtype_c; /* enum tv_dtype */
+    int32_t flags;                     /* reserved, must be 0 */
+    int64_t batch, M, N, K;
+    const void* A; int64_t sa_b, sa_m, sa_k; /* element strides; A already includes the view offset */
+    const void* B; int64_t sb_b, sb_k, sb_n; /* K.permute({0,2,1}) of a [b,n,k] tensor: sb_k = 1, sb_n = k */
+    void*       C; int64_t sc_b, sc_m, sc_n;
+} tv_gemm_args;
+
+/* General batched matmul.  Routes M <= 8 shapes to the GEMV kernels when they serve the
+ * dtype/layout, everything else to the MFMA GEMM kernels (or the SIMT slow path). */
+int tv_hip_gemm(const tv_gemm_args* args, void* hip_stream);
+
+/* Skinny-M (M <= 8) matrix-vector path: HBM-streaming, no matrix cores.  Returns
+ * TV_E_UNSUPPORTED for M > 8 or for a dtype pair it does not serve. */
+int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream);
+
+/* Human-readable text for any return code of this library. */
+const char* tv_hip_strerror(int code);
+
+/* ABI version of this header (bumped on any change of tv_gemm_args or the entry points). */
+int tv_hip_abi_version(void);
+
+/* Test hook: the next `count` calls of tv_hip_gemm / tv_hip_gemv return `code` without touching
+ * the device.  Lets host code prove error propagation without a GPU.  count = 0 disarms. */
+void tv_hip_inject_fault(int code, int count);
+
+#define TV_HIP_ABI_VERSION 1
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TENSORVIA_HIP_H */

@@ -1,0 +1,137 @@
+// extern "C" entry points of libtv_hip.so: argument validation and kernel routing.
+// The argument checks restate the ones ops::Mul performs before dispatch (reference
+// src/ops.cpp:540-556) at the level of a strided descriptor.
+#include <atomic>
+
+#include "tv_kernels.h"
+
+namespace {
+
+std::atomic<int> g_fault_code{0};
+std::atomic<int> g_fault_count{0};
+
+bool take_fault(int* code) {
+    int n = g_fault_count.load();
+    while (n > 0) {
+        if (g_fault_count.compare_exchange_weak(n, n - 1)) {
+            *code = g_fault_code.load();
+            return true;
+        }
+    }
+    return false;
+}
+
+bool is_float_dt(int dt) { return dt == TV_BFLOAT16 || dt == TV_FLOAT16 || dt == TV_FLOAT32 || dt == TV_FLOAT64; }
+
+// Output dtypes each input pair may produce.  For the matrix-core dtypes the GPU-backend result
+// type (compute_type(a, b), reference include/core/type_traits.h:270-287) and the widened CPU
+// backend result (src/backend/cpu/mul.cpp:110-112) are both served; other pairs produce exactly
+// the CPU backend's result type.
+int cpu_result_type(int a, int b) {
+    // CPU widens fp16/bf16 to fp32 first (mul.cpp:110-111), then applies compute_type.
+    if (a == TV_FLOAT16 || a == TV_BFLOAT16) a = TV_FLOAT32;
+    if (b == TV_FLOAT16 || b == TV_BFLOAT16) b = TV_FLOAT32;
+    if (a == b) return a;
+    const bool ai = a <= TV_INT64, bi = b <= TV_INT64;
+    if (ai && bi) return a > b ? a : b;
+    if (!ai && !bi) {
+        int m = a > b ? a : b;
+        return m < TV_FLOAT32 ? TV_FLOAT32 : m;
+    }
+    if (a == TV_INT64 || b == TV_INT64) return TV_FLOAT64;
+    int m = a > b ? a : b;
+    return m < TV_FLOAT32 ? TV_FLOAT32 : m;
+}
+
+bool mfma_pair(const tv_gemm_args* a) {
+    if (a->dtype_a != a->dtype_b) return false;
+    switch (a->dtype_a) {
+        case TV_FLOAT32: return a->dtype_c == TV_FLOAT32;
+        case TV_BFLOAT16: return a->dtype_c == TV_BFLOAT16 || a->dtype_c == TV_FLOAT32;
+        case TV_FLOAT16: return a->dtype_c == TV_FLOAT16 || a->dtype_c == TV_FLOAT32;
+        case TV_INT8: return a->dtype_c == TV_INT8 || a->dtype_c == TV_INT32;
+        default: return false;
+    }
+}
+
+int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
+    if (!a) return TV_E_NULL;
+    if (a->flags != 0) return TV_E_UNSUPPORTED;
+    for (int dt : {a->dtype_a, a->dtype_b, a->dtype_c})
+        if (dt < TV_INT8 || dt > TV_FLOAT64) return TV_E_DTYPE;
+    if (a->batch < 0 || a->M < 0 || a->N < 0 || a->K < 0) return TV_E_SHAPE;
+    const int64_t lim = 0x7FFFFFFF;
+    if (a->batch > lim || a->M > lim || a->N > lim || a->K > lim) return TV_E_SHAPE;
+    if (!mfma_pair(a) && a->dtype_c != cpu_result_type(a->dtype_a, a->dtype_b)) return TV_E_DTYPE;
+    const bool empty = a->batch == 0 || a->M == 0 || a->N == 0;
+    if (!empty) {
+        if (!a->C) return TV_E_NULL;
+        if (a->K > 0 && (!a->A || !a->B)) return TV_E_NULL;
+    }
+    d->A = a->A; d->B = a->B; d->C = a->C;
+    d->sa_b = a->sa_b; d->sa_m = a->sa_m; d->sa_k = a->sa_k;
+    d->sb_b = a->sb_b; d->sb_k = a->sb_k; d->sb_n = a->sb_n;
+    d->sc_b = a->sc_b; d->sc_m = a->sc_m; d->sc_n = a->sc_n;
+    d->M = (int32_t)a->M; d->N = (int32_t)a->N; d->K = (int32_t)a->K; d->batch = (int32_t)a->batch;
+    d->dtype_a = a->dtype_a; d->dtype_b = a->dtype_b; d->dtype_c = a->dtype_c;
+    (void)is_float_dt;
+    return TV_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int tv_hip_abi_version(void) { return TV_HIP_ABI_VERSION; }
+
+void tv_hip_inject_fault(int code, int count) {
+    g_fault_code.store(code);
+    g_fault_count.store(count < 0 ? 0 : count);
+}
+
+int tv_hip_gemm(const tv_gemm_args* args, void* hip_stream) {
+    int code;
+    if (take_fault(&code)) return code;
+    tvk::GemmDesc d;
+    int rc = validate(args, &d);
+    if (rc) return rc;
+    if (d.batch == 0 || d.M == 0 || d.N == 0) return TV_OK;
+    hipStream_t s = static_cast<hipStream_t>(hip_stream);
+    if (mfma_pair(args)) {
+        if (d.M <= 8) {
+            rc = tvk::launch_gemv(d, s);
+            if (rc != TV_E_UNSUPPORTED) return rc;
+        }
+        return tvk::launch_gemm_mfma(d, s);
+    }
+    return tvk::launch_gemm_simt(d, s);
+}
+
+int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream) {
+    int code;
+    if (take_fault(&code)) return code;
+    tvk::GemmDesc d;
+    int rc = validate(args, &d);
+    if (rc) return rc;
+    if (d.M > 8) return TV_E_UNSUPPORTED;
+    if (!mfma_pair(args)) return TV_E_UNSUPPORTED;
+    if (d.batch == 0 || d.M == 0 || d.N == 0) return TV_OK;
+    return tvk::launch_gemv(d, static_cast<hipStream_t>(hip_stream));
+}
+
+const char* tv_hip_strerror(int code) {
+    switch (code) {
+        case TV_OK: return "success";
+        case TV_E_NULL: return "tensorvia-hip: a required pointer is NULL";
+        case TV_E_SHAPE: return "tensorvia-hip: invalid or too large batch/M/N/K";
+        case TV_E_DTYPE: return "tensorvia-hip: dtype out of range or output dtype not allowed for the input dtypes";
+        case TV_E_UNSUPPORTED: return "tensorvia-hip: request not served by this entry point";
+        case TV_E_INJECTED: return "tensorvia-hip: injected fault";
+        case TV_E_NOMEM: return "tensorvia-hip: workspace allocation failed";
+        default: break;
+    }
+    if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+    return "tensorvia-hip: unknown error";
+}
+
+} // extern "C"

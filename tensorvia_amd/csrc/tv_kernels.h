@@ -1,0 +1,60 @@
+// Shared declarations of the gfx950 matmul kernels (device side and launchers).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tensorvia_hip.h"
+
+namespace tvk {
+
+// 16-byte vector types used for global loads, LDS traffic and MFMA operands.
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
+typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
+
+// Descriptor the launchers receive: tv_gemm_args after validation, with sizes narrowed to the
+// ranges the kernels index with.
+struct GemmDesc {
+    const void* A;
+    const void* B;
+    void* C;
+    int64_t sa_b, sa_m, sa_k;
+    int64_t sb_b, sb_k, sb_n;
+    int64_t sc_b, sc_m, sc_n;
+    int32_t M, N, K, batch;
+    int32_t dtype_a, dtype_b, dtype_c;
+};
+
+// Operand load modes for one GEMM operand (A: rows m, B: rows n; "K-contiguous" means the
+// reduction index has stride 1).
+enum LoadMode : int {
+    LOAD_KCONTIG = 0,  // stride 1 along k, 16-byte aligned rows: 16B vector loads
+    LOAD_MNCONTIG = 1, // stride 1 along m (A) / n (B), 16-byte aligned: 16B loads + register transpose
+    LOAD_GENERIC = 2   // anything else: element gathers
+};
+
+// Launchers (return hipError_t, or a negative TV_E_* code).
+int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream);
+int launch_gemm_simt(const GemmDesc& d, hipStream_t stream);
+int launch_gemv(const GemmDesc& d, hipStream_t stream); // TV_E_UNSUPPORTED if it does not serve d
+
+__host__ __device__ inline size_t dtype_size(int dt) {
+    switch (dt) {
+        case TV_INT8: return 1;
+        case TV_INT16: return 2;
+        case TV_INT32: return 4;
+        case TV_INT64: return 8;
+        case TV_BFLOAT16: return 2;
+        case TV_FLOAT16: return 2;
+        case TV_FLOAT32: return 4;
+        case TV_FLOAT64: return 8;
+        default: return 0;
+    }
+}
+
+} // namespace tvk
