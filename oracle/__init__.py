@@ -115,8 +115,15 @@ def threads_used() -> int:
 # ---- brute-force checkers -------------------------------------------------------------------
 
 def exact_int(a: np.ndarray, b: np.ndarray) -> np.ndarray:
-    """Exact integer matmul in int64 (object-free; inputs small enough not to overflow int64)."""
-    return np.matmul(a.astype(np.int64), b.astype(np.int64))
+    """Exact integer matmul as int64.  When every partial sum is below 2^53 in magnitude the fp64
+    BLAS product is exact and is used (fast); otherwise numpy's int64 matmul."""
+    a64, b64 = a.astype(np.int64), b.astype(np.int64)
+    k = a.shape[-1]
+    amax = int(np.abs(a64).max(initial=0))
+    bmax = int(np.abs(b64).max(initial=0))
+    if amax * bmax * max(k, 1) < 2 ** 53:
+        return np.matmul(a64.astype(np.float64), b64.astype(np.float64)).astype(np.int64)
+    return np.matmul(a64, b64)
 
 
 def low_byte(x: np.ndarray) -> np.ndarray:

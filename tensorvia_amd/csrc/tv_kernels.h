@@ -42,6 +42,8 @@ enum LoadMode : int {
 int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream);
 int launch_gemm_simt(const GemmDesc& d, hipStream_t stream);
 int launch_gemv(const GemmDesc& d, hipStream_t stream); // TV_E_UNSUPPORTED if it does not serve d
+// GEMV with an explicit strip width (nl lanes), workgroup size and K split (tuning sweeps).
+int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices);
 
 __host__ __device__ inline size_t dtype_size(int dt) {
     switch (dt) {

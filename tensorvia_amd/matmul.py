@@ -31,6 +31,24 @@ def tv_to_torch(dt: int) -> torch.dtype:
     return _TV2T[dt]
 
 
+def storage_to_torch(arr, dt: int, device="cuda") -> torch.Tensor:
+    """Host storage array (uint16 bit patterns for bf16/fp16) -> torch tensor of tv dtype ``dt``."""
+    import numpy as np
+    arr = np.ascontiguousarray(arr)
+    if dt in (BFLOAT16, FLOAT16):
+        return torch.from_numpy(arr.view(np.int16)).view(tv_to_torch(dt)).to(device)
+    return torch.from_numpy(arr).to(device)
+
+
+def torch_to_storage(t: torch.Tensor):
+    """torch tensor -> host numpy storage array (uint16 bit patterns for bf16/fp16)."""
+    import numpy as np
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
 def compute_type(a: int, b: int) -> int:
     """Result dtype of a binary op (reference include/core/type_traits.h:270-287)."""
     if a == b:

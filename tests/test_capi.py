@@ -1,0 +1,119 @@
+"""C-ABI checks that need no GPU: the library loads, exports every declared symbol, and rejects
+bad descriptors with the documented codes before touching a device."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import tensorvia_amd as tv
+from tensorvia_amd import TvGemmArgs
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^\s*(?:int|void|const char\*)\s+(tv_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_header_declares_the_exported_set():
+    assert declared_functions() == set(tv.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(tv.KERNEL_LIB))
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_matches_header():
+    text = (ROOT / "include" / "tensorvia_hip.h").read_text()
+    v = int(re.search(r"#define TV_HIP_ABI_VERSION (\d+)", text).group(1))
+    assert tv.lib().tv_hip_abi_version() == v
+
+
+def test_struct_layout_matches_c(tmp_path):
+    fields = [f for f, _ in TvGemmArgs._fields_]
+    src = tmp_path / "off.c"
+    src.write_text("#include <stdio.h>\n#include <stddef.h>\n#include \"tensorvia_hip.h\"\nint main(void){\n"
+                   + "".join(f'printf("%zu\\n", offsetof(tv_gemm_args, {f}));\n' for f in fields)
+                   + 'printf("%zu\\n", sizeof(tv_gemm_args));return 0;}\n')
+    exe = tmp_path / "off"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [getattr(TvGemmArgs, f).offset for f in fields] + [ctypes.sizeof(TvGemmArgs)]
+    assert got == want
+
+
+def _args(**kw):
+    a = TvGemmArgs()
+    a.dtype_a = a.dtype_b = a.dtype_c = tv.FLOAT32
+    a.batch, a.M, a.N, a.K = 1, 4, 4, 4
+    a.A, a.B, a.C = 16, 32, 48  # never dereferenced: every case below returns before a launch
+    a.sa_m, a.sa_k, a.sb_k, a.sb_n, a.sc_m, a.sc_n = 4, 1, 4, 1, 4, 1
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _call(fn, a):
+    return getattr(tv.lib(), fn)(ctypes.byref(a), None)
+
+
+@pytest.mark.parametrize("fn", ["tv_hip_gemm", "tv_hip_gemv"])
+def test_rejections(fn):
+    assert getattr(tv.lib(), fn)(None, None) == tv.TV_E_NULL
+    assert _call(fn, _args(dtype_a=9)) == tv.TV_E_DTYPE
+    assert _call(fn, _args(dtype_c=-1)) == tv.TV_E_DTYPE
+    assert _call(fn, _args(dtype_a=tv.INT8, dtype_b=tv.INT8, dtype_c=tv.FLOAT32)) == tv.TV_E_DTYPE
+    assert _call(fn, _args(dtype_a=tv.BFLOAT16, dtype_b=tv.BFLOAT16, dtype_c=tv.FLOAT16)) == tv.TV_E_DTYPE
+    assert _call(fn, _args(M=-1)) == tv.TV_E_SHAPE
+    assert _call(fn, _args(K=1 << 40)) == tv.TV_E_SHAPE
+    assert _call(fn, _args(C=None)) == tv.TV_E_NULL
+    assert _call(fn, _args(A=None)) == tv.TV_E_NULL
+    assert _call(fn, _args(flags=1)) == tv.TV_E_UNSUPPORTED
+    # empty problems are valid no-ops
+    assert _call(fn, _args(M=0, A=None, B=None, C=None)) == tv.TV_OK
+    assert _call(fn, _args(batch=0)) == tv.TV_OK
+
+
+def test_gemv_rejects_large_m_and_non_mfma_pairs():
+    assert _call("tv_hip_gemv", _args(M=9)) == tv.TV_E_UNSUPPORTED
+    assert _call("tv_hip_gemv", _args(dtype_a=tv.INT32, dtype_b=tv.INT32, dtype_c=tv.INT32)) == tv.TV_E_UNSUPPORTED
+
+
+def test_mixed_pairs_must_use_cpu_result_type():
+    # int8 x int16 -> int16 (compute_type); anything else is rejected
+    assert _call("tv_hip_gemm", _args(dtype_a=tv.INT8, dtype_b=tv.INT16, dtype_c=tv.INT8)) == tv.TV_E_DTYPE
+    # bf16 x fp16 -> fp32 (widened on the CPU backend), int64 x fp32 -> fp64
+    assert _call("tv_hip_gemm", _args(dtype_a=tv.BFLOAT16, dtype_b=tv.FLOAT16, dtype_c=tv.BFLOAT16)) == tv.TV_E_DTYPE
+    assert _call("tv_hip_gemm", _args(dtype_a=tv.INT64, dtype_b=tv.FLOAT32, dtype_c=tv.FLOAT32)) == tv.TV_E_DTYPE
+
+
+def test_fault_injection_propagates_and_disarms():
+    L = tv.lib()
+    L.tv_hip_inject_fault(tv.TV_E_INJECTED, 2)
+    a = _args(M=0)
+    assert _call("tv_hip_gemm", a) == tv.TV_E_INJECTED
+    assert _call("tv_hip_gemv", a) == tv.TV_E_INJECTED
+    assert _call("tv_hip_gemm", a) == tv.TV_OK
+    L.tv_hip_inject_fault(7, 1)  # a positive code reads as a hipError_t
+    with pytest.raises(tv.TensorviaHipError) as e:
+        tv.check(_call("tv_hip_gemm", a))
+    assert e.value.code == 7
+    L.tv_hip_inject_fault(0, 0)
+
+
+def test_strerror_covers_codes():
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        s = tv.strerror(code)
+        assert s and "unknown" not in s
+    assert "unknown" in tv.strerror(-99)

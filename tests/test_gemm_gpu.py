@@ -1,0 +1,285 @@
+"""GPU parity: the HIP kernels (through the C-ABI) against the CPU oracle and brute force.
+
+Bars: int8 bit-exact (low byte of the exact sum, or the full int32 sum); fp32 within
+1e-5*sqrt(K) relative to sum_k |a||b|; bf16/fp16 within 1e-2 of the fp32-accumulated value (plus the
+fp32 accumulation allowance); integer-valued float inputs, whose sums every accumulation order
+reproduces exactly, bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from tensorvia_amd import rng
+from tests import golden
+from tests.util import (BFLOAT16, FLOAT16, FLOAT32, INT8, INT32, assert_fp32_close, assert_half_close,
+                        to_f32, to_storage, to_torch)
+
+pytestmark = pytest.mark.gpu
+
+
+def ints(seed, shape, lo, hi, dt=np.float32):
+    return rng.uniform_int(seed, int(np.prod(shape)), lo, hi).astype(dt).reshape(shape)
+
+
+def half_bits(x, dt):
+    return rng.f32_to_bf16_bits(x) if dt == BFLOAT16 else rng.f32_to_f16_bits(x)
+
+
+# ---- golden vectors -------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", sorted(golden.load()))
+def test_golden_bit_exact(hip, name):
+    case = golden.load()[name]
+    dta, dtb, dtc, layout = (int(v) for v in case["meta"])
+    a = to_torch(case["a"], dta)
+    b = to_torch(case["b"], dtb)
+    if layout == 1:
+        b = b.permute(0, 2, 1)  # strided view, consumed without a repack
+    c = hip.gemm(a, b, out_dtype=dtc)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(c), case["c"])
+
+
+# ---- int8 -----------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", [(37, 129, 53), (256, 256, 256), (300, 130, 517), (16, 4096, 16),
+                                   (257, 64, 255), (9, 16, 9), (1000, 2000, 300)])
+def test_int8_vs_oracle_bit_exact(hip, shape):
+    M, K, N = shape
+    a = ints(1, (M, K), -128, 127, np.int8)
+    b = ints(2, (K, N), -128, 127, np.int8)
+    c = hip.gemm(to_torch(a, INT8), to_torch(b, INT8))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(c), orc.mul(a, INT8, b, INT8))
+
+
+def test_int8_int32_output(hip):
+    a = ints(3, (200, 333), -128, 127, np.int8)
+    b = ints(4, (333, 150), -128, 127, np.int8)
+    c = hip.gemm(to_torch(a, INT8), to_torch(b, INT8), out_dtype=INT32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(c), orc.exact_int(a, b).astype(np.int32))
+
+
+def test_int8_known_answers(hip):
+    ones = torch.ones((300, 4096), dtype=torch.int8, device="cuda")
+    c = hip.gemm(ones, ones.t())  # K = 4096 -> 4096 mod 256 = 0; B is an N-contiguous... transposed view
+    torch.cuda.synchronize()
+    assert not c.any().item()
+    eye = torch.eye(260, dtype=torch.int8, device="cuda")
+    b = to_torch(ints(5, (260, 190), -128, 127, np.int8), INT8)
+    c = hip.gemm(eye, b)
+    torch.cuda.synchronize()
+    assert torch.equal(c, b)
+
+
+def test_int8_config2_full_size_sampled(hip):
+    """c2: int8 [4096,4096] @ [4096,4096], uniform ints in [-10,10]; 128 sampled rows and columns
+    against exact int64 sums, plus the full row/column checksum identity mod 256."""
+    n = 4096
+    a = ints(3, (n, n), -10, 10, np.int8)
+    b = ints(4, (n, n), -10, 10, np.int8)
+    c = to_storage(hip.gemm(to_torch(a, INT8), to_torch(b, INT8)))
+    r = np.random.default_rng(0)
+    rows = r.choice(n, 128, replace=False)
+    cols = r.choice(n, 128, replace=False)
+    np.testing.assert_array_equal(c[rows], orc.low_byte(orc.exact_int(a[rows], b)))
+    np.testing.assert_array_equal(c[:, cols], orc.low_byte(orc.exact_int(a, b[:, cols])))
+    # checksum of checksums: sum_ij C_ij == (1^T A)(B 1) mod 256 for the exact sums
+    lhs = int(c.astype(np.int64).sum()) % 256
+    rhs = int((a.astype(np.int64).sum(0) * b.astype(np.int64).sum(1)).sum()) % 256
+    assert lhs == rhs
+
+
+# ---- fp32 -----------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", [(45, 77, 61), (128, 128, 128), (2592 // 8, 2048 // 8, 4096 // 8), (129, 257, 65)])
+def test_fp32_integer_inputs_bit_exact(hip, shape):
+    M, K, N = shape
+    a = ints(6, (M, K), -8, 8)
+    b = ints(7, (K, N), -8, 8)
+    c = hip.gemm(to_torch(a, FLOAT32), to_torch(b, FLOAT32))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(c), orc.mul(a, FLOAT32, b, FLOAT32))
+
+
+@pytest.mark.parametrize("shape", [(300, 512, 200), (64, 2048, 96)])
+def test_fp32_uniform_vs_oracle(hip, shape):
+    M, K, N = shape
+    a = rng.uniform_f32(8, M * K, -1, 1).reshape(M, K)
+    b = rng.uniform_f32(9, K * N, -1, 1).reshape(K, N)
+    c = to_storage(hip.gemm(to_torch(a, FLOAT32), to_torch(b, FLOAT32)))
+    assert_fp32_close(c, orc.mul(a, FLOAT32, b, FLOAT32), orc.abs_bound(a, b), K)
+
+
+def test_fp32_config1_full_size_sampled(hip):
+    """c1: fp32 [2592,2048] @ [2048,4096] U[-1,1]: sampled rows/columns against fp64 sums."""
+    M, K, N = 2592, 2048, 4096
+    a = rng.uniform_f32(1, M * K, -1, 1).reshape(M, K)
+    b = rng.uniform_f32(2, K * N, -1, 1).reshape(K, N)
+    c = to_storage(hip.gemm(to_torch(a, FLOAT32), to_torch(b, FLOAT32)))
+    r = np.random.default_rng(1)
+    rows = r.choice(M, 64, replace=False)
+    cols = r.choice(N, 64, replace=False)
+    assert_fp32_close(c[rows], orc.f64_matmul(a[rows], b), orc.abs_bound(a[rows], b), K)
+    assert_fp32_close(c[:, cols], orc.f64_matmul(a, b[:, cols]), orc.abs_bound(a, b[:, cols]), K)
+
+
+# ---- bf16 / fp16 ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16])
+@pytest.mark.parametrize("shape", [(33, 40, 72), (256, 512, 256), (300, 200, 136)])
+def test_half_integer_inputs_bit_exact(hip, dt, shape):
+    M, K, N = shape
+    x = ints(10, (M, K), -3, 3)
+    y = ints(11, (K, N), -3, 3)
+    ref = orc.mul(half_bits(x, dt), dt, half_bits(y, dt), dt)  # exact fp32 sums
+    c = hip.gemm(to_torch(half_bits(x, dt), dt), to_torch(half_bits(y, dt), dt))
+    c32 = hip.gemm(to_torch(half_bits(x, dt), dt), to_torch(half_bits(y, dt), dt), out_dtype=FLOAT32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(c), half_bits(ref, dt))
+    np.testing.assert_array_equal(to_storage(c32), ref)
+
+
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16])
+def test_half_uniform_vs_oracle(hip, dt):
+    M, K, N = 200, 1024, 328
+    x = half_bits(rng.uniform_f32(12, M * K, -1, 1), dt).reshape(M, K)
+    y = half_bits(rng.uniform_f32(13, K * N, -1, 1), dt).reshape(K, N)
+    ref = orc.mul(x, dt, y, dt)
+    c = to_f32(to_storage(hip.gemm(to_torch(x, dt), to_torch(y, dt))), dt)
+    assert_half_close(c, ref, orc.abs_bound(to_f32(x, dt), to_f32(y, dt)), K)
+
+
+def test_bf16_config3_broadcast_equals_flattened(hip):
+    """c3 at reduced batch: A[4,2048,4096] @ B[4096,4096] (B broadcast, batch stride 0) equals the
+    flattened call [4*2048,4096] @ [4096,4096] bit for bit, and sampled rows match the oracle."""
+    Bt, M, K, N = 4, 2048, 4096, 4096
+    a = rng.make("uniform", (Bt, M, K), 5, "bfloat16")
+    b = rng.make("uniform", (K, N), 6, "bfloat16")
+    ta, tb = to_torch(a, BFLOAT16), to_torch(b, BFLOAT16)
+    c3 = hip.gemm(ta, tb)
+    c2 = hip.gemm(ta.reshape(Bt * M, K), tb)
+    torch.cuda.synchronize()
+    assert torch.equal(c3.reshape(Bt * M, N), c2)
+    c = to_f32(to_storage(c3), BFLOAT16).reshape(Bt * M, N)
+    rows = np.random.default_rng(2).choice(Bt * M, 32, replace=False)
+    xa = a.reshape(Bt * M, K)[rows]
+    ref = orc.mul(xa, BFLOAT16, b, BFLOAT16)
+    assert_half_close(c[rows], ref, orc.abs_bound(to_f32(xa, BFLOAT16), to_f32(b, BFLOAT16)), K)
+
+
+def test_fp16_config4_transposed_view(hip):
+    """c4 at reduced batch: Q[4,2048,128] @ K.permute(0,2,1) consumed through strides, against the
+    oracle on the materialised transpose (ops::Transpose(K,{0,2,1}) on the CPU)."""
+    Bt, S, D = 4, 2048, 128
+    q = half_bits(rng.normal_f32(7, Bt * S * D) / np.float32(np.sqrt(D)), FLOAT16).reshape(Bt, S, D)
+    k = half_bits(rng.normal_f32(8, Bt * S * D) / np.float32(np.sqrt(D)), FLOAT16).reshape(Bt, S, D)
+    tq, tk = to_torch(q, FLOAT16), to_torch(k, FLOAT16)
+    view = tk.permute(0, 2, 1)
+    assert view.stride() == (S * D, 1, D)
+    c = to_f32(to_storage(hip.gemm(tq, view)), FLOAT16)
+    kt = orc.transpose_last2(k)
+    ref = orc.mul(q, FLOAT16, kt, FLOAT16)
+    bound = orc.abs_bound(to_f32(q, FLOAT16)[0], to_f32(kt, FLOAT16)[0])
+    assert_half_close(c[0], ref[0], bound, D)
+    for bi in range(1, Bt):
+        assert_half_close(c[bi], ref[bi], orc.abs_bound(to_f32(q, FLOAT16)[bi], to_f32(kt, FLOAT16)[bi]), D)
+
+
+# ---- views, offsets, batches ----------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", [FLOAT32, BFLOAT16, INT8])
+def test_views_offsets_and_layouts(hip, dt):
+    """Sliced (offset) operands, transposed A and B, non-unit inner strides (gather path) and batched
+    B all give the oracle's result on the equivalent dense inputs."""
+    lo, hi = (-3, 3)
+    M, K, N = 80, 96, 96
+    big_a = ints(20, (M + 5, K + 16), lo, hi)
+    big_b = ints(21, (K + 8, N + 24), lo, hi)
+
+    def dev(x):
+        if dt == INT8:
+            return to_torch(x.astype(np.int8), INT8)
+        if dt == BFLOAT16:
+            return to_torch(rng.f32_to_bf16_bits(x), BFLOAT16)
+        return to_torch(x, FLOAT32)
+
+    def ref_of(a, b):
+        if dt == INT8:
+            return orc.mul(a.astype(np.int8), INT8, b.astype(np.int8), INT8)
+        out = orc.mul(a.astype(np.float32), FLOAT32, b.astype(np.float32), FLOAT32)
+        return rng.f32_to_bf16_bits(out) if dt == BFLOAT16 else out
+
+    ta, tb = dev(big_a), dev(big_b)
+    cases = {
+        "offset": (ta[3:3 + M, 8:8 + K], tb[4:4 + K, 16:16 + N], big_a[3:3 + M, 8:8 + K], big_b[4:4 + K, 16:16 + N]),
+        "a_transposed": (dev(np.ascontiguousarray(big_a[:M, :K].T)).t(), tb[:K, :N], big_a[:M, :K], big_b[:K, :N]),
+        "b_transposed": (ta[:M, :K], dev(np.ascontiguousarray(big_b[:K, :N].T)).t(), big_a[:M, :K], big_b[:K, :N]),
+        "gather_a": (ta[:M, 0:2 * (K // 2):2], tb[:K // 2, :N], big_a[:M, 0:2 * (K // 2):2], big_b[:K // 2, :N]),
+        "gather_b": (ta[:M, :K // 2], tb[0:K:2, 1:N + 1], big_a[:M, :K // 2], big_b[0:K:2, 1:N + 1]),
+        "odd_offset": (ta[1:1 + M, 1:1 + K], tb[1:1 + K, 1:1 + N], big_a[1:1 + M, 1:1 + K], big_b[1:1 + K, 1:1 + N]),
+    }
+    for name, (x, y, xa, ya) in cases.items():
+        c = hip.gemm(x, y)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_storage(c), ref_of(np.ascontiguousarray(xa), np.ascontiguousarray(ya)),
+                                      err_msg=name)
+
+
+@pytest.mark.parametrize("dt", [FLOAT32, FLOAT16, INT8])
+def test_batched_equal_batches(hip, dt):
+    Bt, M, K, N = 3, 50, 130, 40
+    x = ints(22, (Bt, M, K), -3, 3)
+    y = ints(23, (Bt, K, N), -3, 3)
+    if dt == INT8:
+        xs, ys = x.astype(np.int8), y.astype(np.int8)
+    elif dt == FLOAT16:
+        xs, ys = rng.f32_to_f16_bits(x), rng.f32_to_f16_bits(y)
+    else:
+        xs, ys = x, y
+    c = to_storage(hip.gemm(to_torch(xs, dt), to_torch(ys, dt)))
+    ref = orc.mul(xs, dt, ys, dt)
+    if dt == FLOAT16:
+        ref = rng.f32_to_f16_bits(ref)
+    np.testing.assert_array_equal(c, ref)
+
+
+def test_output_view_with_strides(hip):
+    a = ints(24, (40, 64), -3, 3)
+    b = ints(25, (64, 48), -3, 3)
+    big = torch.zeros((50, 100), dtype=torch.float32, device="cuda")
+    out = big[5:45, 10:58]
+    hip.gemm(to_torch(a, FLOAT32), to_torch(b, FLOAT32), out=out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(out), orc.mul(a, FLOAT32, b, FLOAT32))
+    assert big[:5].abs().sum().item() == 0 and big[:, :10].abs().sum().item() == 0
+
+
+# ---- SIMT path (dtype pairs without matrix cores) ---------------------------------------------
+
+@pytest.mark.parametrize("pair", [("int32", "int32"), ("int16", "int16"), ("int64", "int64"),
+                                  ("int8", "int16"), ("int32", "float32"), ("float64", "float64")])
+@pytest.mark.parametrize("shape", [(20, 130, 30), (1024, 70, 1024)])
+def test_simt_pairs_vs_oracle(hip, pair, shape):
+    import oracle
+    names = {"int8": 0, "int16": 1, "int32": 2, "int64": 3, "float32": 6, "float64": 7}
+    da, db = names[pair[0]], names[pair[1]]
+    M, K, N = shape
+    a = ints(26, (M, K), -50, 50, np.dtype(pair[0]))
+    b = ints(27, (K, N), -50, 50, np.dtype(pair[1]))
+    ref = oracle.mul(a, da, b, db)
+    c = hip.gemm(to_torch(a, da), to_torch(b, db), out_dtype=oracle.result_type(da, db))
+    torch.cuda.synchronize()
+    got = to_storage(c)
+    if ref.dtype.kind == "f":
+        np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6 * np.abs(ref).max())
+    else:
+        np.testing.assert_array_equal(got, ref)
+
+
+def test_rejects_bad_output_dtype(hip):
+    a = torch.ones((4, 4), dtype=torch.int8, device="cuda")
+    with pytest.raises(hip.TensorviaHipError):
+        hip.gemm(a, a, out_dtype=FLOAT32)

@@ -1,0 +1,95 @@
+"""GPU parity of the skinny-M (decode) path: x[M<=8, K] @ W[K, N] through tv_hip_gemv, against the
+oracle (mul_kernel_basic restated, which is what the reference runs for these shapes)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from tensorvia_amd import rng
+from tests.util import BFLOAT16, FLOAT16, FLOAT32, INT8, INT32, assert_fp32_close, assert_half_close, to_f32, to_storage, to_torch
+
+pytestmark = pytest.mark.gpu
+
+
+def half_bits(x, dt):
+    return rng.f32_to_bf16_bits(x) if dt == BFLOAT16 else rng.f32_to_f16_bits(x)
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_config5_bf16_full_size(hip, M):
+    """c5: x[M,4096] N(0,1) @ W[4096,11008] U[-0.05,0.05], bf16, fp32 accumulate, bf16 out."""
+    K, N = 4096, 11008
+    x = rng.make("normal", (M, K), 9 if M == 1 else 11, "bfloat16")
+    w = rng.make("uniform", (K, N), 10, "bfloat16", lo=-0.05, hi=0.05)
+    c = to_f32(to_storage(hip.gemv(to_torch(x, BFLOAT16), to_torch(w, BFLOAT16))), BFLOAT16)
+    ref = orc.mul(x, BFLOAT16, w, BFLOAT16)
+    assert_half_close(c, ref, orc.abs_bound(to_f32(x, BFLOAT16), to_f32(w, BFLOAT16)), K)
+    # deterministic split-K reduction: a second call gives identical bits
+    c2 = to_f32(to_storage(hip.gemv(to_torch(x, BFLOAT16), to_torch(w, BFLOAT16))), BFLOAT16)
+    np.testing.assert_array_equal(c, c2)
+
+
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, FLOAT32, INT8])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("KN", [(64, 128), (4096, 1008), (1024, 11008), (16, 32)])
+def test_gemv_integer_inputs_exact(hip, dt, M, KN):
+    K, N = KN
+    if dt == INT8:
+        x = rng.uniform_int(30, M * K, -128, 127).astype(np.int8).reshape(M, K)
+        w = rng.uniform_int(31, K * N, -128, 127).astype(np.int8).reshape(K, N)
+        c = hip.gemv(to_torch(x, INT8), to_torch(w, INT8))
+        c32 = hip.gemv(to_torch(x, INT8), to_torch(w, INT8), out_dtype=INT32)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_storage(c), orc.mul(x, INT8, w, INT8))
+        np.testing.assert_array_equal(to_storage(c32), orc.exact_int(x, w).astype(np.int32))
+        return
+    x = rng.uniform_int(32, M * K, -2, 2).astype(np.float32).reshape(M, K)
+    w = rng.uniform_int(33, K * N, -2, 2).astype(np.float32).reshape(K, N)
+    if dt == FLOAT32:
+        xs, ws = x, w
+    else:
+        xs, ws = half_bits(x, dt), half_bits(w, dt)
+    ref = orc.mul(xs, dt, ws, dt)  # exact: |sum| <= 4K
+    c = to_storage(hip.gemv(to_torch(xs, dt), to_torch(ws, dt)))
+    want = ref if dt == FLOAT32 else half_bits(ref, dt)
+    np.testing.assert_array_equal(c, want)
+
+
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT32])
+def test_gemv_uniform_vs_oracle(hip, dt):
+    M, K, N = 4, 2048, 3000
+    x = rng.normal_f32(40, M * K).reshape(M, K)
+    w = rng.uniform_f32(41, K * N, -0.05, 0.05).reshape(K, N)
+    xs, ws = (x, w) if dt == FLOAT32 else (half_bits(x, dt), half_bits(w, dt))
+    ref = orc.mul(xs, dt, ws, dt)
+    c = to_f32(to_storage(hip.gemv(to_torch(xs, dt), to_torch(ws, dt))), dt)
+    bound = orc.abs_bound(to_f32(xs, dt), to_f32(ws, dt))
+    (assert_fp32_close if dt == FLOAT32 else assert_half_close)(c, ref, bound, K)
+
+
+def test_gemv_batched_and_broadcast(hip):
+    Bt, M, K, N = 3, 2, 512, 256
+    x = rng.uniform_int(42, Bt * M * K, -2, 2).astype(np.float32).reshape(Bt, M, K)
+    w = rng.uniform_int(43, K * N, -2, 2).astype(np.float32).reshape(K, N)
+    xb, wb = rng.f32_to_bf16_bits(x), rng.f32_to_bf16_bits(w)
+    c = to_storage(hip.gemv(to_torch(xb, BFLOAT16), to_torch(wb, BFLOAT16)))
+    ref = orc.mul(xb.reshape(Bt * M, K), BFLOAT16, wb, BFLOAT16).reshape(Bt, M, N)
+    np.testing.assert_array_equal(c, rng.f32_to_bf16_bits(ref))
+    w3 = np.stack([w, -w, 2 * w])
+    c3 = to_storage(hip.gemv(to_torch(xb, BFLOAT16), to_torch(rng.f32_to_bf16_bits(w3), BFLOAT16)))
+    ref3 = orc.mul(xb, BFLOAT16, rng.f32_to_bf16_bits(w3), BFLOAT16)
+    np.testing.assert_array_equal(c3, rng.f32_to_bf16_bits(ref3))
+
+
+def test_gemv_unsupported_layouts_report_and_gemm_serves_them(hip):
+    K, N = 256, 64
+    x = rng.uniform_int(44, K, -2, 2).astype(np.float32).reshape(1, K)
+    w = rng.uniform_int(45, K * N, -2, 2).astype(np.float32).reshape(K, N)
+    wt = to_torch(np.ascontiguousarray(w.T), FLOAT32).t()  # K-contiguous W
+    with pytest.raises(hip.TensorviaHipError) as e:
+        hip.gemv(to_torch(x, FLOAT32), wt)
+    assert e.value.code == hip.TV_E_UNSUPPORTED
+    c = to_storage(hip.gemm(to_torch(x, FLOAT32), wt))
+    np.testing.assert_array_equal(c, orc.mul(x, FLOAT32, w, FLOAT32))
+    with pytest.raises(hip.TensorviaHipError):
+        hip.gemv(to_torch(np.zeros((9, K), np.float32), FLOAT32), to_torch(w, FLOAT32))
