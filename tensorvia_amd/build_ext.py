@@ -27,7 +27,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Packed fp32 ALU ops stay disabled (the compiler would otherwise form v_pk_*_f32 from float code).
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
-KERNEL_SOURCES = ["gemm_mfma.hip", "gemv.hip", "gemm_simt.hip", "capi.hip"]
+KERNEL_SOURCES = ["gemm_mfma_f32.hip", "gemm_mfma_bf16.hip", "gemm_mfma_f16.hip", "gemm_mfma_i8.hip",
+                  "gemm_dispatch.hip", "gemv.hip", "gemm_simt.hip", "capi.hip"]
 
 
 def _run(cmd: list[str], verbose: bool) -> None:
@@ -52,7 +53,7 @@ def _stale(target: Path, deps: list[Path]) -> bool:
 def build_kernels(verbose: bool = False, force: bool = True) -> Path:
     """Compile libtv_hip.so (the extern "C" kernel library) for ``ARCH``."""
     BUILD.mkdir(exist_ok=True)
-    headers = [INCLUDE / "tensorvia_hip.h", CSRC / "tv_kernels.h"]
+    headers = [INCLUDE / "tensorvia_hip.h", CSRC / "tv_kernels.h", CSRC / "gemm_mfma_impl.h"]
     jobs = []
     objs = []
     for src in KERNEL_SOURCES:

@@ -1,0 +1,557 @@
+// MFMA GEMM kernels for gfx950 (CDNA4): fp32, bf16, fp16 and int8 inputs (template code; one
+// translation unit per input dtype instantiates it: gemm_mfma_{f32,bf16,f16,i8}.hip).
+//
+// Replaces the 16x16 shared-memory tile kernel mul_cuda_3d (reference src/backend/cuda/mul.cu:8-48)
+// and computes what MulImpl<CPU> computes (src/backend/cpu/mul.cpp:27-85) for these dtypes:
+//   C[b,m,n] = sum_k A[b,m,k] * B[b,k,n]
+// with fp32 accumulation for the float types and exact int32 accumulation for int8.
+//
+// Design:
+//  * One workgroup computes a BM x BN output tile; its waves are laid out WAVES_M x WAVES_N and
+//    each wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile made of 16x16 MFMA blocks.  The 16-bit
+//    and int8 tiles run 8 waves (two per SIMD, 256 registers each) so one wave's LDS and HBM
+//    latency hides behind the other's MFMAs.
+//  * Every dtype streams 128-byte k-slices: an LDS tile row holds BK = 128/sizeof(T) consecutive
+//    k values of one m (A) or one n (B).  A lane feeds the matrix core one 16-byte fragment per
+//    operand per "k-group" (4 lane groups x 16 bytes = 64 bytes of k); a BK slice is 2 k-groups.
+//      fp32 : 4 x v_mfma_f32_16x16x4_f32 per fragment pair
+//      bf16 : 1 x v_mfma_f32_16x16x32_bf16
+//      fp16 : 1 x v_mfma_f32_16x16x32_f16
+//      int8 : 1 x v_mfma_i32_16x16x64_i8
+//    A and B lanes use the same (lane group, element) -> k assignment, so the k order inside a
+//    fragment does not affect the dot product.  The B fragment is passed as the instruction's
+//    first operand, so each lane's 4 results are 4 consecutive n of one m (vector stores).
+//  * LDS rows are 128 bytes; the eight 16-byte chunks of row r are XOR-swizzled with
+//    (r ^ (r >> 4)) & 7 so the fragment reads (16 consecutive rows, one chunk) and the transposing
+//    stores (rows 4/8/16 apart) spread over the banks.
+//  * Software pipeline, one barrier per k-tile (two LDS stages, fragments double-buffered):
+//      phase A: MFMAs on k-group 0 of tile t, interleaved with the LDS stores of tile t+1 (from
+//               registers), the fragment reads of k-group 1 and the buffer loads of tile t+2;
+//      barrier (LDS-only fence: the global prefetches stay in flight);
+//      phase B: MFMAs on k-group 1, interleaved with the fragment reads of k-group 0 of tile t+1.
+//  * Operands are read through their element strides (views are never repacked):
+//      K-contiguous rows           -> 16-byte buffer loads straight into the LDS layout
+//      M/N-contiguous (transposed) -> 16-byte buffer loads of 4 k-rows, transposed in registers
+//      any other strides           -> element gathers
+//    Buffer loads return zero outside [0, num_records), which zero-fills the M/N/K tails without
+//    branches.
+//  * Batch and broadcast: the batch offset is b*s_b, so s_b = 0 broadcasts an operand.
+//  * Workgroup ids are remapped so that tiles that share A rows / B columns run on the same XCD
+//    (workgroups are dealt round-robin over the 8 XCDs, each with its own L2).
+#pragma once
+#include "tv_kernels.h"
+
+namespace tvk {
+
+// ---------------------------------------------------------------------------------------------
+// Matrix-core step per input dtype: c += a (x) b with a = B fragment, b = A fragment.
+template <typename T> struct Mfma;
+
+template <> struct Mfma<float> {
+    using Acc = f32x4;
+    __device__ static inline void run(const u32x4& a, const u32x4& b, Acc& c) {
+        const f32x4 av = __builtin_bit_cast(f32x4, a);
+        const f32x4 bv = __builtin_bit_cast(f32x4, b);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(av[0], bv[0], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(av[1], bv[1], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(av[2], bv[2], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(av[3], bv[3], c, 0, 0, 0);
+    }
+    static constexpr int kInstr = 4;
+};
+template <> struct Mfma<__bf16> {
+    using Acc = f32x4;
+    __device__ static inline void run(const u32x4& a, const u32x4& b, Acc& c) {
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+    static constexpr int kInstr = 1;
+};
+template <> struct Mfma<_Float16> {
+    using Acc = f32x4;
+    __device__ static inline void run(const u32x4& a, const u32x4& b, Acc& c) {
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+    static constexpr int kInstr = 1;
+};
+template <> struct Mfma<int8_t> {
+    using Acc = i32x4;
+    __device__ static inline void run(const u32x4& a, const u32x4& b, Acc& c) {
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a),
+                                                  __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+    }
+    static constexpr int kInstr = 1;
+};
+
+// ---------------------------------------------------------------------------------------------
+// Raw element access inside a 16-byte register chunk.
+template <int ES> __device__ inline unsigned elem_bits(const u32x4& r, int e) {
+    if constexpr (ES == 4) return r[e];
+    else if constexpr (ES == 2) return (r[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+    else return (r[e >> 2] >> (8 * (e & 3))) & 0xFFu;
+}
+template <int ES> __device__ inline void set_elem_bits(u32x4& r, int e, unsigned v) {
+    if constexpr (ES == 4) r[e] = v;
+    else if constexpr (ES == 2) r[e >> 1] |= (v & 0xFFFFu) << (16 * (e & 1));
+    else r[e >> 2] |= (v & 0xFFu) << (8 * (e & 3));
+}
+template <int ES> __device__ inline unsigned load_bits(const char* p) {
+    if constexpr (ES == 4) return *reinterpret_cast<const unsigned*>(p);
+    else if constexpr (ES == 2) return *reinterpret_cast<const unsigned short*>(p);
+    else return *reinterpret_cast<const unsigned char*>(p);
+}
+
+// LDS tile layout: row r (one m of A or one n of B) holds 128 bytes of k as eight 16-byte chunks,
+// chunk c stored at position c ^ swz(r).  swz uses row bits 3..8 only, so rows 8q..8q+7 share it:
+//  * fragment reads take 16 rows spaced FM (or FN) apart, whose bits 3..5 all differ -> the 8
+//    lanes of each 128-byte read cycle hit 8 different chunks (no bank conflicts), and the 8
+//    fragments of a wave differ only in bits 0..2 -> one base address plus an immediate offset;
+//  * transposing stores write rows VEC apart from lanes that differ in rc -> (2rc ^ rc/4) spreads
+//    16 lanes over 8 chunks.
+__device__ inline int lds_swz(int row) { return ((row >> 3) ^ (row >> 6)) & 7; }
+__device__ inline int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ lds_swz(row)) << 4); }
+
+// A lane offset at or above 2^31 is outside every buffer resource built below (num_records <= 2^30),
+// also after a chunk's stride multiple (< 2^30) is added to it.
+constexpr unsigned kOOB = 0x80000000u;
+
+__device__ inline u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const char* base, int64_t bytes) {
+    const int nr = bytes <= 0 ? 0 : (bytes > 0x40000000 ? 0x40000000 : (int)bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, nr, 0x00020000);
+}
+
+// Keeps the compiler from hoisting values derived from `v` out of a loop (they are cheaper to
+// recompute than to hold in registers across the MFMA loop).
+__device__ inline int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// One operand's global -> register -> LDS path.  ROWS is BM (operand A, rows = m) or BN
+// (operand B, rows = n); s_r / s_k are the element strides along rows and along k.
+//
+// Vector modes: a lane loads chunk j at  lane_off + j * (wave-uniform stride)  from the k-tile
+// origin.  Tails are zero-filled by the buffer range check: the resource ends where the valid
+// rows (K-contiguous) or the valid k rows (M/N-contiguous) end, and a lane whose k range
+// (K-contiguous) or row (M/N-contiguous) lies outside gets an offset >= 2^31.
+template <int MODE, int ROWS, int THREADS, int ES>
+struct TileLoader {
+    static constexpr int VEC = 16 / ES;            // elements per 16-byte chunk
+    static constexpr int BK = 128 / ES;            // k extent of one LDS row
+    static constexpr int NCH = ROWS * 8 / THREADS; // 16-byte registers per thread
+    static constexpr int RC = ROWS / VEC;          // 16-byte row chunks across the tile (MN mode)
+    static_assert(NCH >= 1 && ROWS * 8 % THREADS == 0, "tile rows do not divide over the threads");
+    static_assert(MODE != LOAD_MNCONTIG || (NCH % 4 == 0 && THREADS % RC == 0), "transposing loads need 4 k-rows");
+
+    const char* base;  // element (row0, k = 0) of this tile, as bytes
+    int64_t s_r, s_k;  // element strides
+    int rows_valid;    // rows of this tile inside the matrix
+    int K;
+
+    // K-contiguous: chunk j = tile row (tid>>3) + j*THREADS/8, k = (tid&7)*VEC.
+    // M/N-contiguous: chunk j = (blk = j/4, q = j%4): rows (tid%RC)*VEC.., k = (tid/RC + blk*THREADS/RC)*4 + q.
+    __device__ inline unsigned lane_off(int t) const {
+        if constexpr (MODE == LOAD_MNCONTIG) return (unsigned)(((int64_t)(t / RC) * 4 * s_k + (t % RC) * VEC) * ES);
+        else return (unsigned)(((int64_t)(t >> 3) * s_r + (t & 7) * VEC) * ES);
+    }
+    __device__ inline int64_t chunk_stride(int j) const {
+        if constexpr (MODE == LOAD_MNCONTIG) return ((int64_t)(j / 4) * 4 * (THREADS / RC) + (j % 4)) * s_k * ES;
+        else return (int64_t)j * (THREADS / 8) * s_r * ES;
+    }
+
+    __device__ inline void load(int t, int k0, u32x4 (&r)[NCH]) const {
+        if constexpr (MODE == LOAD_GENERIC) {
+#pragma unroll
+            for (int j = 0; j < NCH; ++j) {
+                const int lin = t + j * THREADS;
+                const int row = lin >> 3, c = lin & 7;
+                u32x4 v = {0, 0, 0, 0};
+                if (row < rows_valid) {
+                    const char* p = base + (int64_t)row * s_r * ES;
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) {
+                        const int k = k0 + c * VEC + e;
+                        if (k < K) set_elem_bits<ES>(v, e, load_bits<ES>(p + (int64_t)k * s_k * ES));
+                    }
+                }
+                r[j] = v;
+            }
+        } else {
+            const int rows = rows_valid < ROWS ? rows_valid : ROWS;
+            const char* kbase;
+            int64_t bytes;
+            unsigned lo;
+            if constexpr (MODE == LOAD_MNCONTIG) {
+                kbase = base + (int64_t)k0 * s_k * ES;
+                bytes = (int64_t)(K - k0) * s_k * ES;              // k rows k0..K-1
+                lo = (t % RC) * VEC < rows ? lane_off(t) : kOOB;  // whole chunk of rows valid or not
+            } else {
+                kbase = base + (int64_t)k0 * ES;
+                bytes = (int64_t)rows * s_r * ES;                  // rows 0..rows-1
+                lo = k0 + (t & 7) * VEC < K ? lane_off(t) : kOOB;
+            }
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(kbase, bytes);
+#pragma unroll
+            for (int j = 0; j < NCH; ++j) r[j] = buf_load16(rs, lo + (unsigned)chunk_stride(j));
+        }
+    }
+
+    __device__ inline void store(int t, char* lds, const u32x4 (&r)[NCH]) const {
+        if constexpr (MODE == LOAD_MNCONTIG) {
+#pragma unroll
+            for (int blk = 0; blk < NCH / 4; ++blk) {
+                const int rc = t % RC, kb = t / RC + blk * (THREADS / RC);
+                const u32x4& r0 = r[blk * 4 + 0];
+                const u32x4& r1 = r[blk * 4 + 1];
+                const u32x4& r2 = r[blk * 4 + 2];
+                const u32x4& r3 = r[blk * 4 + 3];
+                const int byte_in_row = kb * 4 * ES; // 4 consecutive k per piece
+                const int chunk = byte_in_row >> 4, within = byte_in_row & 15;
+                // rows rc*VEC + e: swz depends on e only through e >> 3
+                char* dst0 = lds + lds_off(rc * VEC, chunk) + within;
+                char* dst8 = VEC > 8 ? lds + lds_off(rc * VEC + 8, chunk) + within - 8 * 128 : dst0;
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    char* dst = (e < 8 ? dst0 : dst8) + e * 128;
+                    if constexpr (ES == 4) {
+                        *reinterpret_cast<u32x4*>(dst) = u32x4{r0[e], r1[e], r2[e], r3[e]};
+                    } else if constexpr (ES == 2) {
+                        const unsigned lo = elem_bits<2>(r0, e) | (elem_bits<2>(r1, e) << 16);
+                        const unsigned hi = elem_bits<2>(r2, e) | (elem_bits<2>(r3, e) << 16);
+                        *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
+                    } else {
+                        *reinterpret_cast<unsigned*>(dst) = elem_bits<1>(r0, e) | (elem_bits<1>(r1, e) << 8) |
+                                                            (elem_bits<1>(r2, e) << 16) | (elem_bits<1>(r3, e) << 24);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NCH; ++j) {
+                const int lin = t + j * THREADS;
+                *reinterpret_cast<u32x4*>(lds + lds_off(lin >> 3, lin & 7)) = r[j];
+            }
+        }
+    }
+
+    // LDS store instructions one store() issues per thread.
+    static constexpr int kStores = MODE == LOAD_MNCONTIG ? (NCH / 4) * VEC : NCH;
+};
+
+// ---------------------------------------------------------------------------------------------
+template <typename T_, int BM_, int BN_, int WAVES_M_, int WAVES_N_, int AMODE_, int BMODE_>
+struct GemmCfg {
+    using T = T_;
+    static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+    static constexpr int AMODE = AMODE_, BMODE = BMODE_;
+    static constexpr int ES = sizeof(T);
+    static constexpr int BK = 128 / ES;
+    static constexpr int THREADS = WAVES_M * WAVES_N * 64;
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+    static constexpr int FM = WM / 16, FN = WN / 16;
+    static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile must be whole 16x16 blocks");
+};
+
+// Output conversion.  int8 output keeps the low byte of the exact int32 sum (two's-complement
+// wrap), the reference CPU backend's int8 result; half outputs round to nearest even.
+template <typename TC, typename V> __device__ inline TC cvt_out(V v) { return static_cast<TC>(v); }
+
+// Store the wave's accumulators as TC: row r = row0 + q*FM + i (q < 4, i < FM), columns col0..col0+FN-1
+// from acc[i][0..FN-1][q].
+template <typename TC, class C, typename Acc>
+__device__ inline void write_tile(const Acc (&acc)[C::FM][C::FN], char* Cb, int row0, int col0, bool vec_ok,
+                                  const GemmDesc& d) {
+    typedef TC vec_t __attribute__((__vector_size__(C::FN * sizeof(TC))));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i) {
+            const int row = row0 + q * C::FM + i;
+            if (row >= d.M) continue;
+            TC* crow = reinterpret_cast<TC*>(Cb) + (int64_t)row * d.sc_m;
+            if (vec_ok) {
+                vec_t v;
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j) v[j] = cvt_out<TC>(acc[i][j][q]);
+                if constexpr (sizeof(vec_t) <= 16) {
+                    *reinterpret_cast<vec_t*>(crow + col0) = v;
+                } else {
+                    // 32-byte rows (fp32/int32 with FN = 8): two 16-byte stores.
+                    typedef TC half_t __attribute__((__vector_size__(16)));
+                    constexpr int H = 16 / sizeof(TC);
+                    half_t lo, hi;
+#pragma unroll
+                    for (int j = 0; j < H; ++j) { lo[j] = v[j]; hi[j] = v[H + j]; }
+                    reinterpret_cast<half_t*>(crow + col0)[0] = lo;
+                    reinterpret_cast<half_t*>(crow + col0)[1] = hi;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j)
+                    if (col0 + j < d.N) crow[(int64_t)(col0 + j) * d.sc_n] = cvt_out<TC>(acc[i][j][q]);
+            }
+        }
+    }
+}
+
+// Scheduling hints for the interleaved phases (LLVM AMDGPU sched_group_barrier masks).
+constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200, SG_VALU = 0x002;
+
+// Workgroup barrier that orders LDS only (global prefetches stay in flight).  The scheduling
+// fences keep each phase's MFMAs on their side of the barrier.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <class C>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
+                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
+void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec) {
+    using T = typename C::T;
+    using Op = Mfma<T>;
+    using Acc = typename Op::Acc;
+    constexpr int ES = C::ES;
+
+    __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+
+    // Workgroup -> tile.  The hardware deals workgroup ids round-robin over the 8 XCDs; undo that
+    // so that a contiguous range of logical tiles lands on one XCD, then walk tiles in groups of
+    // `group_m` tile-rows so neighbouring workgroups share A rows and B columns in that XCD's L2.
+    int bid = blockIdx.x;
+    const int nwg = gridDim.x;
+    if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+    const int per_batch = tiles_m * tiles_n;
+    const int b = bid / per_batch;
+    int r = bid - b * per_batch;
+    const int span = group_m * tiles_n;
+    const int g = r / span;
+    const int first_m = g * group_m;
+    const int gsz = min(tiles_m - first_m, group_m);
+    r -= g * span;
+    const int tm = first_m + r % gsz;
+    const int tn = r / gsz;
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
+
+    TileLoader<C::AMODE, C::BM, C::THREADS, ES> la;
+    la.base = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + (int64_t)m0 * d.sa_m) * ES;
+    la.s_r = d.sa_m; la.s_k = d.sa_k; la.rows_valid = d.M - m0; la.K = d.K;
+    TileLoader<C::BMODE, C::BN, C::THREADS, ES> lb;
+    lb.base = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)n0 * d.sb_n) * ES;
+    lb.s_r = d.sb_n; lb.s_k = d.sb_k; lb.rows_valid = d.N - n0; lb.K = d.K;
+
+    Acc acc[C::FM][C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+
+    u32x4 ra[decltype(la)::NCH];
+    u32x4 rb[decltype(lb)::NCH];
+    // B fragments of a k-group are held for the whole group; A fragments stream one 16-row block at
+    // a time, one block ahead of the MFMAs that use them.
+    u32x4 fb[C::FN];
+    u32x4 fa;
+
+    // Fragment f of a wave covers tile rows w*W + lane_row*F + f (F = FM or FN): the 16 lane rows
+    // are F apart, so all fragments share one swizzle and differ by f * 128 bytes.
+    static_assert((C::FM == 4 || C::FM == 8) && (C::FN == 4 || C::FN == 8), "fragment interleave needs 4 or 8");
+    const int frag_row = lane & 15, frag_grp = lane >> 4;
+    const int a_row0 = wm * C::WM + frag_row * C::FM;
+    const int b_row0 = wn * C::WN + frag_row * C::FN;
+    const int a_off[2] = {lds_off(a_row0, frag_grp), lds_off(a_row0, 4 + frag_grp)};
+    const int b_off[2] = {C::A_BYTES + lds_off(b_row0, frag_grp), C::A_BYTES + lds_off(b_row0, 4 + frag_grp)};
+    auto a_frag = [&](const char* stage, int kg, int i) {
+        return *reinterpret_cast<const u32x4*>(stage + a_off[kg] + i * 128);
+    };
+    auto b_frag = [&](const char* stage, int kg, int j) {
+        return *reinterpret_cast<const u32x4*>(stage + b_off[kg] + j * 128);
+    };
+    // MFMAs of one k-group (B fragments in fb, first A fragment already in `fa`).  While A block i
+    // is multiplied, A block i+1 is read; in the last block each B fragment is refilled with the
+    // following group's right after its last use, and the first A block of that group is read.
+    auto kgroup = [&](const char* stage, int kg, const char* nstage, int nkg) {
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i) {
+            const u32x4 a_cur = fa;
+            fa = (i + 1 < C::FM) ? a_frag(stage, kg, i + 1) : a_frag(nstage, nkg, 0);
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) {
+                Op::run(a_cur, fb[j], acc[i][j]);
+                if (i + 1 == C::FM) fb[j] = b_frag(nstage, nkg, j);
+            }
+        }
+    };
+
+    const int nk = (d.K + C::BK - 1) / C::BK;
+    // Prologue: tile 0 -> LDS stage 0, tile 1 -> registers, k-group 0 fragments of tile 0.
+    la.load(tid, 0, ra);
+    lb.load(tid, 0, rb);
+    la.store(tid, smem, ra);
+    lb.store(tid, smem + C::A_BYTES, rb);
+    la.load(tid, C::BK, ra);
+    lb.load(tid, C::BK, rb);
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) fb[j] = b_frag(smem, 0, j);
+    fa = a_frag(smem, 0, 0);
+
+    constexpr int NMF = C::FM * C::FN * Op::kInstr;                  // MFMAs per k-group
+    constexpr int NST = decltype(la)::kStores + decltype(lb)::kStores; // LDS stores per tile
+    constexpr int NRD = C::FM + C::FN;                                // fragment reads per k-group
+    constexpr int NLD = decltype(la)::NCH + decltype(lb)::NCH;        // buffer loads per tile
+
+    for (int kt = 0; kt < nk; ++kt) {
+        char* cur = smem + (kt & 1) * C::STAGE;
+        char* nxt = smem + ((kt + 1) & 1) * C::STAGE;
+        // Phase A: tile kt+1 -> LDS, tile kt+2 -> registers, MFMAs of k-group 0 of tile kt
+        // (reading k-group 1's fragments of tile kt on the way).
+        const int t = opaque(tid);
+        la.store(t, nxt, ra);
+        lb.store(t, nxt + C::A_BYTES, rb);
+        la.load(t, (kt + 2) * C::BK, ra);
+        lb.load(t, (kt + 2) * C::BK, rb);
+        kgroup(cur, 0, cur, 1);
+        if constexpr (NMF >= NRD + NLD + 1) {
+            constexpr int slots = NMF - NRD - NLD;            // MFMAs left for the LDS stores
+            constexpr int wper = (NST + slots - 1) / slots;   // stores per MFMA
+            constexpr int wgroups = (NST + wper - 1) / wper;
+#pragma unroll
+            for (int i = 0; i < wgroups; ++i) {
+                __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, wper, 0);
+                __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < NLD; ++i) {
+                __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < NRD; ++i) {
+                __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+            }
+            if constexpr (NMF - wgroups - NRD - NLD > 0)
+                __builtin_amdgcn_sched_group_barrier(SG_MFMA, NMF - wgroups - NRD - NLD, 0);
+        }
+        lds_barrier();
+        // Phase B: MFMAs of k-group 1 of tile kt, reading k-group 0's fragments of tile kt+1.
+        kgroup(cur, 1, nxt, 0);
+        if constexpr (NMF >= NRD) {
+#pragma unroll
+            for (int i = 0; i < NRD; ++i) {
+                __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, NMF - NRD, 0);
+        }
+    }
+    (void)SG_VALU;
+
+    // Epilogue.  acc[i][j][q] = C[m0 + wm*WM + (4*(lane/16) + q)*FM + i][n0 + wn*WN + (lane%16)*FN + j]:
+    // for each (i, q) a lane holds FN consecutive columns of one row -> one vector store.  The output
+    // type is chosen once; each branch is straight-line code over the accumulators.
+    const size_t csz = dtype_size(d.dtype_c);
+    char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
+    const int col0 = n0 + wn * C::WN + (lane & 15) * C::FN;
+    const int row0 = m0 + wm * C::WM + (lane >> 4) * 4 * C::FM;
+    const bool vec_ok = c_vec && col0 + C::FN <= d.N;
+    if constexpr (__is_same(Acc, i32x4)) {
+        if (d.dtype_c == TV_INT8) write_tile<int8_t, C>(acc, Cb, row0, col0, vec_ok, d);
+        else write_tile<int32_t, C>(acc, Cb, row0, col0, vec_ok, d);
+    } else {
+        if (d.dtype_c == TV_BFLOAT16) write_tile<__bf16, C>(acc, Cb, row0, col0, vec_ok, d);
+        else if (d.dtype_c == TV_FLOAT16) write_tile<_Float16, C>(acc, Cb, row0, col0, vec_ok, d);
+        else write_tile<float, C>(acc, Cb, row0, col0, vec_ok, d);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side: pick the operand load modes and the tile configuration.
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Mode for one operand.  `rows` extent R, strides s_r (along rows), s_k (along k), s_b (batch).
+// The vector modes also need every per-lane offset inside one k-tile panel to fit in 31 bits.
+static int pick_mode(const void* p, int64_t R, int64_t K, int64_t s_r, int64_t s_k, int64_t s_b, int64_t batch,
+                     int es, int rows_tile) {
+    const int64_t vec = 16 / es;
+    const int64_t bk = 128 / es;
+    const bool ok_ptr = aligned16(p);
+    const bool ok_b = batch <= 1 || s_b % vec == 0;
+    const int64_t lim = (int64_t)1 << 30;
+    // Tails are masked by the buffer range check, which needs rows (k rows) that do not overlap.
+    if (s_k == 1 && ok_ptr && ok_b && K % vec == 0 && (R <= 1 || (s_r % vec == 0 && s_r >= K)) &&
+        ((int64_t)rows_tile * s_r + bk) * es < lim)
+        return LOAD_KCONTIG;
+    if (s_r == 1 && ok_ptr && ok_b && R % vec == 0 && (K <= 1 || (s_k % vec == 0 && s_k >= R)) &&
+        (bk * s_k + rows_tile) * es < lim)
+        return LOAD_MNCONTIG;
+    return LOAD_GENERIC;
+}
+
+template <class C>
+static int run_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
+    const int tiles_m = (d.M + C::BM - 1) / C::BM;
+    const int tiles_n = (d.N + C::BN - 1) / C::BN;
+    const int64_t nwg = (int64_t)tiles_m * tiles_n * d.batch;
+    if (nwg <= 0) return 0;
+    if (nwg > 0x7FFFFFFF) return TV_E_SHAPE;
+    const size_t csz = dtype_size(d.dtype_c);
+    // Vector stores of FN elements (aligned to FN elements, at most 16 bytes) along rows of C.
+    const int64_t fn = C::FN;
+    const size_t valign = fn * csz < 16 ? fn * csz : 16;
+    const int c_vec = d.sc_n == 1 && d.sc_m % fn == 0 && (d.batch <= 1 || d.sc_b % fn == 0) &&
+                      (reinterpret_cast<uintptr_t>(d.C) % valign) == 0;
+    hipLaunchKernelGGL(gemm_mfma_kernel<C>, dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
+                       group_m, c_vec);
+    return hipGetLastError();
+}
+
+// Tile shapes: the large tile serves the vector load modes; any operand that needs element
+// gathers runs a 128x128 tile (fewer registers, faster to build, rarely used).
+template <typename T, int BM, int BN, int WMW, int WNW>
+static int run_modes(const GemmDesc& d, hipStream_t stream, int group_m) {
+    const int es = (int)sizeof(T);
+    const int am = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, BM);
+    const int bm = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, BN);
+#define TV_CASE(A_, B_) \
+    if (am == A_ && bm == B_) return run_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream, group_m);
+    TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)
+    TV_CASE(LOAD_KCONTIG, LOAD_KCONTIG)
+    TV_CASE(LOAD_MNCONTIG, LOAD_MNCONTIG)
+    TV_CASE(LOAD_MNCONTIG, LOAD_KCONTIG)
+#undef TV_CASE
+    // Gather paths: re-pick the modes for the small tile's row count.
+    const int am2 = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, 128);
+    const int bm2 = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, 128);
+#define TV_CASE(A_, B_) \
+    if (am2 == A_ && bm2 == B_) return run_cfg<GemmCfg<T, 128, 128, 2, 2, A_, B_>>(d, stream, group_m);
+    TV_CASE(LOAD_KCONTIG, LOAD_GENERIC)
+    TV_CASE(LOAD_MNCONTIG, LOAD_GENERIC)
+    TV_CASE(LOAD_GENERIC, LOAD_MNCONTIG)
+    TV_CASE(LOAD_GENERIC, LOAD_KCONTIG)
+    TV_CASE(LOAD_GENERIC, LOAD_GENERIC)
+    TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)
+    TV_CASE(LOAD_KCONTIG, LOAD_KCONTIG)
+    TV_CASE(LOAD_MNCONTIG, LOAD_MNCONTIG)
+    TV_CASE(LOAD_MNCONTIG, LOAD_KCONTIG)
+#undef TV_CASE
+    return TV_E_UNSUPPORTED;
+}
+
+} // namespace tvk
