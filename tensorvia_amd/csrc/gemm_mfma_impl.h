@@ -11,30 +11,34 @@
 //    each wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile made of 16x16 MFMA blocks.  The 16-bit
 //    and int8 tiles run 8 waves (two per SIMD, 256 registers each) so one wave's LDS and HBM
 //    latency hides behind the other's MFMAs.
-//  * Every dtype streams 128-byte k-slices: an LDS tile row holds BK = 128/sizeof(T) consecutive
-//    k values of one m (A) or one n (B).  A lane feeds the matrix core one 16-byte fragment per
-//    operand per "k-group" (4 lane groups x 16 bytes = 64 bytes of k); a BK slice is 2 k-groups.
+//  * Every dtype streams 128-byte k-slices (BK = 128/sizeof(T) values of k per tile step).  A lane
+//    feeds the matrix core one 16-byte fragment per operand per "k-group" (4 lane groups x 16
+//    bytes = 64 bytes of k); a k-slice is 2 k-groups.
 //      fp32 : 4 x v_mfma_f32_16x16x4_f32 per fragment pair
 //      bf16 : 1 x v_mfma_f32_16x16x32_bf16
 //      fp16 : 1 x v_mfma_f32_16x16x32_f16
 //      int8 : 1 x v_mfma_i32_16x16x64_i8
 //    A and B lanes use the same (lane group, element) -> k assignment, so the k order inside a
-//    fragment does not affect the dot product.  The B fragment is passed as the instruction's
-//    first operand, so each lane's 4 results are 4 consecutive n of one m (vector stores).
-//  * LDS rows are 128 bytes; the eight 16-byte chunks of row r are XOR-swizzled with
-//    (r ^ (r >> 4)) & 7 so the fragment reads (16 consecutive rows, one chunk) and the transposing
-//    stores (rows 4/8/16 apart) spread over the banks.
-//  * Software pipeline, one barrier per k-tile (two LDS stages, fragments double-buffered):
+//    fragment does not affect the dot product.  The B fragment is the instruction's first operand,
+//    so each lane's 4 results are 4 consecutive n of one m (vector stores).
+//  * Each operand is copied into LDS in its own memory order, 16 bytes per lane, never
+//    transposed in registers:
+//      K-contiguous operand   -> LDS rows of 128 bytes of k (one row per m or n); fragments are
+//                                ds_read_b128; 16-byte chunk c of row r sits at c ^ ((r >> 1) & 7),
+//                                so the 16 rows of a fragment read cover all 64 banks once.
+//      M/N-contiguous operand -> LDS rows of one k each (all m or n of the tile, padded by 16/32
+//                                bytes so consecutive k rows start in different banks); fragments
+//                                are gathered by the gfx950 transpose reads ds_read_b64_tr_b16 /
+//                                ds_read_b64_tr_b8 (fp32: four ds_read_b32), which hand each lane
+//                                the k values of one column.
+//      any other strides      -> element gathers into the K-contiguous layout
+//    Buffer loads return zero outside the resource's range, which zero-fills the M/N/K tails
+//    without branches.
+//  * Software pipeline, one barrier per k-tile (two LDS stages):
 //      phase A: MFMAs on k-group 0 of tile t, interleaved with the LDS stores of tile t+1 (from
-//               registers), the fragment reads of k-group 1 and the buffer loads of tile t+2;
+//               registers), the buffer loads of tile t+2 and the fragment reads of k-group 1;
 //      barrier (LDS-only fence: the global prefetches stay in flight);
 //      phase B: MFMAs on k-group 1, interleaved with the fragment reads of k-group 0 of tile t+1.
-//  * Operands are read through their element strides (views are never repacked):
-//      K-contiguous rows           -> 16-byte buffer loads straight into the LDS layout
-//      M/N-contiguous (transposed) -> 16-byte buffer loads of 4 k-rows, transposed in registers
-//      any other strides           -> element gathers
-//    Buffer loads return zero outside [0, num_records), which zero-fills the M/N/K tails without
-//    branches.
 //  * Batch and broadcast: the batch offset is b*s_b, so s_b = 0 broadcasts an operand.
 //  * Workgroup ids are remapped so that tiles that share A rows / B columns run on the same XCD
 //    (workgroups are dealt round-robin over the 8 XCDs, each with its own L2).
@@ -102,15 +106,8 @@ template <int ES> __device__ inline unsigned load_bits(const char* p) {
     else return *reinterpret_cast<const unsigned char*>(p);
 }
 
-// LDS tile layout: row r (one m of A or one n of B) holds 128 bytes of k as eight 16-byte chunks,
-// chunk c stored at position c ^ swz(r).  swz uses row bits 3..8 only, so rows 8q..8q+7 share it:
-//  * fragment reads take 16 rows spaced FM (or FN) apart, whose bits 3..5 all differ -> the 8
-//    lanes of each 128-byte read cycle hit 8 different chunks (no bank conflicts), and the 8
-//    fragments of a wave differ only in bits 0..2 -> one base address plus an immediate offset;
-//  * transposing stores write rows VEC apart from lanes that differ in rc -> (2rc ^ rc/4) spreads
-//    16 lanes over 8 chunks.
-__device__ inline int lds_swz(int row) { return ((row >> 3) ^ (row >> 6)) & 7; }
-__device__ inline int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ lds_swz(row)) << 4); }
+// K-contiguous LDS layout: row r holds 128 bytes of k; 16-byte chunk c is stored at c ^ ((r>>1)&7).
+__device__ inline int kc_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
 // A lane offset at or above 2^31 is outside every buffer resource built below (num_records <= 2^30),
 // also after a chunk's stride multiple (< 2^30) is added to it.
@@ -131,36 +128,44 @@ __device__ inline int opaque(int v) {
     return v;
 }
 
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+typedef __attribute__((address_space(3))) i32x2_t lds_i32x2;
+typedef __attribute__((address_space(3))) char lds_char;
+
 // ---------------------------------------------------------------------------------------------
-// One operand's global -> register -> LDS path.  ROWS is BM (operand A, rows = m) or BN
-// (operand B, rows = n); s_r / s_k are the element strides along rows and along k.
+// One operand's global -> register -> LDS -> fragment path.  ROWS is BM (operand A, rows = m) or
+// BN (operand B, rows = n); s_r / s_k are the element strides along rows and along k.
 //
 // Vector modes: a lane loads chunk j at  lane_off + j * (wave-uniform stride)  from the k-tile
 // origin.  Tails are zero-filled by the buffer range check: the resource ends where the valid
 // rows (K-contiguous) or the valid k rows (M/N-contiguous) end, and a lane whose k range
-// (K-contiguous) or row (M/N-contiguous) lies outside gets an offset >= 2^31.
+// (K-contiguous) or row range (M/N-contiguous) lies outside gets an offset >= 2^31.
 template <int MODE, int ROWS, int THREADS, int ES>
 struct TileLoader {
     static constexpr int VEC = 16 / ES;            // elements per 16-byte chunk
-    static constexpr int BK = 128 / ES;            // k extent of one LDS row
+    static constexpr int BK = 128 / ES;            // k extent of one k-tile
     static constexpr int NCH = ROWS * 8 / THREADS; // 16-byte registers per thread
-    static constexpr int RC = ROWS / VEC;          // 16-byte row chunks across the tile (MN mode)
+    static constexpr int RCH = ROWS / VEC;         // 16-byte chunks across one k row (MN layout)
+    static constexpr int PITCH = ROWS * ES + (ES == 4 ? 16 : 32); // MN layout: bytes per k row
+    static constexpr int BYTES = MODE == LOAD_MNCONTIG ? BK * PITCH : ROWS * 128;
     static_assert(NCH >= 1 && ROWS * 8 % THREADS == 0, "tile rows do not divide over the threads");
-    static_assert(MODE != LOAD_MNCONTIG || (NCH % 4 == 0 && THREADS % RC == 0), "transposing loads need 4 k-rows");
+    static_assert(MODE != LOAD_MNCONTIG || THREADS % RCH == 0, "k rows must divide over the threads");
 
     const char* base;  // element (row0, k = 0) of this tile, as bytes
     int64_t s_r, s_k;  // element strides
     int rows_valid;    // rows of this tile inside the matrix
     int K;
 
-    // K-contiguous: chunk j = tile row (tid>>3) + j*THREADS/8, k = (tid&7)*VEC.
-    // M/N-contiguous: chunk j = (blk = j/4, q = j%4): rows (tid%RC)*VEC.., k = (tid/RC + blk*THREADS/RC)*4 + q.
+    // K-contiguous: chunk j = tile row (t>>3) + j*THREADS/8, k = (t&7)*VEC.
+    // M/N-contiguous: chunk j = k row t/RCH + j*THREADS/RCH, rows (t%RCH)*VEC ...
     __device__ inline unsigned lane_off(int t) const {
-        if constexpr (MODE == LOAD_MNCONTIG) return (unsigned)(((int64_t)(t / RC) * 4 * s_k + (t % RC) * VEC) * ES);
+        if constexpr (MODE == LOAD_MNCONTIG) return (unsigned)(((int64_t)(t / RCH) * s_k + (t % RCH) * VEC) * ES);
         else return (unsigned)(((int64_t)(t >> 3) * s_r + (t & 7) * VEC) * ES);
     }
     __device__ inline int64_t chunk_stride(int j) const {
-        if constexpr (MODE == LOAD_MNCONTIG) return ((int64_t)(j / 4) * 4 * (THREADS / RC) + (j % 4)) * s_k * ES;
+        if constexpr (MODE == LOAD_MNCONTIG) return (int64_t)j * (THREADS / RCH) * s_k * ES;
         else return (int64_t)j * (THREADS / 8) * s_r * ES;
     }
 
@@ -188,11 +193,11 @@ struct TileLoader {
             unsigned lo;
             if constexpr (MODE == LOAD_MNCONTIG) {
                 kbase = base + (int64_t)k0 * s_k * ES;
-                bytes = (int64_t)(K - k0) * s_k * ES;              // k rows k0..K-1
-                lo = (t % RC) * VEC < rows ? lane_off(t) : kOOB;  // whole chunk of rows valid or not
+                bytes = (int64_t)(K - k0) * s_k * ES;                   // k rows k0..K-1
+                lo = (t % RCH) * VEC < rows ? lane_off(t) : kOOB;       // whole chunk of rows valid or not
             } else {
                 kbase = base + (int64_t)k0 * ES;
-                bytes = (int64_t)rows * s_r * ES;                  // rows 0..rows-1
+                bytes = (int64_t)rows * s_r * ES;                       // rows 0..rows-1
                 lo = k0 + (t & 7) * VEC < K ? lane_off(t) : kOOB;
             }
             const __amdgpu_buffer_rsrc_t rs = make_rsrc(kbase, bytes);
@@ -203,44 +208,66 @@ struct TileLoader {
 
     __device__ inline void store(int t, char* lds, const u32x4 (&r)[NCH]) const {
         if constexpr (MODE == LOAD_MNCONTIG) {
+            char* dst = lds + (t / RCH) * PITCH + (t % RCH) * 16;
 #pragma unroll
-            for (int blk = 0; blk < NCH / 4; ++blk) {
-                const int rc = t % RC, kb = t / RC + blk * (THREADS / RC);
-                const u32x4& r0 = r[blk * 4 + 0];
-                const u32x4& r1 = r[blk * 4 + 1];
-                const u32x4& r2 = r[blk * 4 + 2];
-                const u32x4& r3 = r[blk * 4 + 3];
-                const int byte_in_row = kb * 4 * ES; // 4 consecutive k per piece
-                const int chunk = byte_in_row >> 4, within = byte_in_row & 15;
-                // rows rc*VEC + e: swz depends on e only through e >> 3
-                char* dst0 = lds + lds_off(rc * VEC, chunk) + within;
-                char* dst8 = VEC > 8 ? lds + lds_off(rc * VEC + 8, chunk) + within - 8 * 128 : dst0;
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    char* dst = (e < 8 ? dst0 : dst8) + e * 128;
-                    if constexpr (ES == 4) {
-                        *reinterpret_cast<u32x4*>(dst) = u32x4{r0[e], r1[e], r2[e], r3[e]};
-                    } else if constexpr (ES == 2) {
-                        const unsigned lo = elem_bits<2>(r0, e) | (elem_bits<2>(r1, e) << 16);
-                        const unsigned hi = elem_bits<2>(r2, e) | (elem_bits<2>(r3, e) << 16);
-                        *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
-                    } else {
-                        *reinterpret_cast<unsigned*>(dst) = elem_bits<1>(r0, e) | (elem_bits<1>(r1, e) << 8) |
-                                                            (elem_bits<1>(r2, e) << 16) | (elem_bits<1>(r3, e) << 24);
-                    }
-                }
-            }
+            for (int j = 0; j < NCH; ++j) *reinterpret_cast<u32x4*>(dst + j * (THREADS / RCH) * PITCH) = r[j];
         } else {
 #pragma unroll
             for (int j = 0; j < NCH; ++j) {
                 const int lin = t + j * THREADS;
-                *reinterpret_cast<u32x4*>(lds + lds_off(lin >> 3, lin & 7)) = r[j];
+                *reinterpret_cast<u32x4*>(lds + kc_off(lin >> 3, lin & 7)) = r[j];
             }
         }
     }
 
-    // LDS store instructions one store() issues per thread.
-    static constexpr int kStores = MODE == LOAD_MNCONTIG ? (NCH / 4) * VEC : NCH;
+    // Fragment addressing.  Fragment f of a wave covers the 16 tile rows w0 + 16f .. w0 + 16f + 15;
+    // lane (row = lane%16, group = lane/16) receives the 16 bytes of k-group kg that the matrix
+    // core expects: k = kg*4*VEC + group*VEC + (0..VEC-1).
+    int fbase[2]; // per k-group: lane byte offset inside a stage (fragment f adds f * frag_step)
+    static constexpr int frag_step = MODE == LOAD_MNCONTIG ? 16 * ES : 16 * 128;
+
+    __device__ inline void frag_init(int lane, int w0) {
+        const int fr = lane & 15, grp = lane >> 4;
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg) {
+            if constexpr (MODE == LOAD_MNCONTIG) {
+                const int kb = kg * 4 * VEC + grp * VEC; // first k of this lane group
+                if constexpr (ES == 2)      // tr16: lanes 4r+c read k row kb+r, rows w0+4c..+3
+                    fbase[kg] = (kb + (fr >> 2)) * PITCH + (w0 + 4 * (fr & 3)) * 2;
+                else if constexpr (ES == 1) // tr8: lanes 2r+c read k row kb+r, rows w0+8c..+7
+                    fbase[kg] = (kb + (fr >> 1)) * PITCH + (w0 + 8 * (fr & 1));
+                else                        // fp32: lane reads k rows kb..kb+3 at row w0+fr
+                    fbase[kg] = kb * PITCH + (w0 + fr) * 4;
+            } else {
+                fbase[kg] = kc_off(w0 + fr, kg * 4 + grp);
+            }
+        }
+    }
+
+    __device__ inline u32x4 frag(const char* stage, int kg, int f) const {
+        const char* p = stage + fbase[kg] + f * frag_step;
+        if constexpr (MODE != LOAD_MNCONTIG) {
+            return *reinterpret_cast<const u32x4*>(p);
+        } else if constexpr (ES == 2) {
+            const lds_char* q = (const lds_char*)p;
+            const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)q);
+            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(q + 4 * PITCH));
+            const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+            return u32x4{l2.x, l2.y, h2.x, h2.y};
+        } else if constexpr (ES == 1) {
+            const lds_char* q = (const lds_char*)p;
+            const i32x2_t lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)q);
+            const i32x2_t hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(q + 8 * PITCH));
+            return u32x4{(unsigned)lo.x, (unsigned)lo.y, (unsigned)hi.x, (unsigned)hi.y};
+        } else {
+            const unsigned* u = reinterpret_cast<const unsigned*>(p);
+            return u32x4{u[0], u[PITCH / 4], u[2 * PITCH / 4], u[3 * PITCH / 4]};
+        }
+    }
+
+    // LDS instructions per thread: stores per tile, reads per fragment.
+    static constexpr int kStores = NCH;
+    static constexpr int kFragReads = MODE == LOAD_MNCONTIG ? (ES == 4 ? 4 : 2) : 1;
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -254,7 +281,8 @@ struct GemmCfg {
     static constexpr int THREADS = WAVES_M * WAVES_N * 64;
     static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     static constexpr int FM = WM / 16, FN = WN / 16;
-    static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+    static constexpr int A_BYTES = (TileLoader<AMODE_, BM_, WAVES_M_ * WAVES_N_ * 64, sizeof(T_)>::BYTES + 15) / 16 * 16;
+    static constexpr int B_BYTES = (TileLoader<BMODE_, BN_, WAVES_M_ * WAVES_N_ * 64, sizeof(T_)>::BYTES + 15) / 16 * 16;
     static constexpr int STAGE = A_BYTES + B_BYTES;
     static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile must be whole 16x16 blocks");
 };
@@ -263,39 +291,29 @@ struct GemmCfg {
 // wrap), the reference CPU backend's int8 result; half outputs round to nearest even.
 template <typename TC, typename V> __device__ inline TC cvt_out(V v) { return static_cast<TC>(v); }
 
-// Store the wave's accumulators as TC: row r = row0 + q*FM + i (q < 4, i < FM), columns col0..col0+FN-1
-// from acc[i][0..FN-1][q].
+// Store the wave's accumulators as TC: acc[i][j][q] is C[row0 + 16i][col0 + 16j + q] (the lane's
+// row and first column are folded into row0 / col0), four consecutive columns per vector store.
 template <typename TC, class C, typename Acc>
 __device__ inline void write_tile(const Acc (&acc)[C::FM][C::FN], char* Cb, int row0, int col0, bool vec_ok,
                                   const GemmDesc& d) {
-    typedef TC vec_t __attribute__((__vector_size__(C::FN * sizeof(TC))));
+    typedef TC vec_t __attribute__((__vector_size__(4 * sizeof(TC))));
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int i = 0; i < C::FM; ++i) {
+        const int row = row0 + 16 * i;
+        if (row >= d.M) continue;
+        TC* crow = reinterpret_cast<TC*>(Cb) + (int64_t)row * d.sc_m;
 #pragma unroll
-        for (int i = 0; i < C::FM; ++i) {
-            const int row = row0 + q * C::FM + i;
-            if (row >= d.M) continue;
-            TC* crow = reinterpret_cast<TC*>(Cb) + (int64_t)row * d.sc_m;
-            if (vec_ok) {
+        for (int j = 0; j < C::FN; ++j) {
+            const int col = col0 + 16 * j;
+            if (vec_ok && col + 4 <= d.N) {
                 vec_t v;
 #pragma unroll
-                for (int j = 0; j < C::FN; ++j) v[j] = cvt_out<TC>(acc[i][j][q]);
-                if constexpr (sizeof(vec_t) <= 16) {
-                    *reinterpret_cast<vec_t*>(crow + col0) = v;
-                } else {
-                    // 32-byte rows (fp32/int32 with FN = 8): two 16-byte stores.
-                    typedef TC half_t __attribute__((__vector_size__(16)));
-                    constexpr int H = 16 / sizeof(TC);
-                    half_t lo, hi;
-#pragma unroll
-                    for (int j = 0; j < H; ++j) { lo[j] = v[j]; hi[j] = v[H + j]; }
-                    reinterpret_cast<half_t*>(crow + col0)[0] = lo;
-                    reinterpret_cast<half_t*>(crow + col0)[1] = hi;
-                }
+                for (int q = 0; q < 4; ++q) v[q] = cvt_out<TC>(acc[i][j][q]);
+                *reinterpret_cast<vec_t*>(crow + col) = v;
             } else {
 #pragma unroll
-                for (int j = 0; j < C::FN; ++j)
-                    if (col0 + j < d.N) crow[(int64_t)(col0 + j) * d.sc_n] = cvt_out<TC>(acc[i][j][q]);
+                for (int q = 0; q < 4; ++q)
+                    if (col + q < d.N) crow[(int64_t)(col + q) * d.sc_n] = cvt_out<TC>(acc[i][j][q]);
             }
         }
     }
@@ -368,20 +386,10 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
     u32x4 fb[C::FN];
     u32x4 fa;
 
-    // Fragment f of a wave covers tile rows w*W + lane_row*F + f (F = FM or FN): the 16 lane rows
-    // are F apart, so all fragments share one swizzle and differ by f * 128 bytes.
-    static_assert((C::FM == 4 || C::FM == 8) && (C::FN == 4 || C::FN == 8), "fragment interleave needs 4 or 8");
-    const int frag_row = lane & 15, frag_grp = lane >> 4;
-    const int a_row0 = wm * C::WM + frag_row * C::FM;
-    const int b_row0 = wn * C::WN + frag_row * C::FN;
-    const int a_off[2] = {lds_off(a_row0, frag_grp), lds_off(a_row0, 4 + frag_grp)};
-    const int b_off[2] = {C::A_BYTES + lds_off(b_row0, frag_grp), C::A_BYTES + lds_off(b_row0, 4 + frag_grp)};
-    auto a_frag = [&](const char* stage, int kg, int i) {
-        return *reinterpret_cast<const u32x4*>(stage + a_off[kg] + i * 128);
-    };
-    auto b_frag = [&](const char* stage, int kg, int j) {
-        return *reinterpret_cast<const u32x4*>(stage + b_off[kg] + j * 128);
-    };
+    la.frag_init(lane, wm * C::WM);
+    lb.frag_init(lane, wn * C::WN);
+    auto a_frag = [&](const char* stage, int kg, int i) { return la.frag(stage, kg, i); };
+    auto b_frag = [&](const char* stage, int kg, int j) { return lb.frag(stage + C::A_BYTES, kg, j); };
     // MFMAs of one k-group (B fragments in fb, first A fragment already in `fa`).  While A block i
     // is multiplied, A block i+1 is read; in the last block each B fragment is refilled with the
     // following group's right after its last use, and the first A block of that group is read.
@@ -392,7 +400,7 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
             fa = (i + 1 < C::FM) ? a_frag(stage, kg, i + 1) : a_frag(nstage, nkg, 0);
 #pragma unroll
             for (int j = 0; j < C::FN; ++j) {
-                Op::run(a_cur, fb[j], acc[i][j]);
+                Op::run(fb[j], a_cur, acc[i][j]);
                 if (i + 1 == C::FM) fb[j] = b_frag(nstage, nkg, j);
             }
         }
@@ -413,7 +421,7 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
 
     constexpr int NMF = C::FM * C::FN * Op::kInstr;                  // MFMAs per k-group
     constexpr int NST = decltype(la)::kStores + decltype(lb)::kStores; // LDS stores per tile
-    constexpr int NRD = C::FM + C::FN;                                // fragment reads per k-group
+    constexpr int NRD = C::FM * decltype(la)::kFragReads + C::FN * decltype(lb)::kFragReads; // LDS reads per k-group
     constexpr int NLD = decltype(la)::NCH + decltype(lb)::NCH;        // buffer loads per tile
 
     for (int kt = 0; kt < nk; ++kt) {
@@ -463,14 +471,13 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
     }
     (void)SG_VALU;
 
-    // Epilogue.  acc[i][j][q] = C[m0 + wm*WM + (4*(lane/16) + q)*FM + i][n0 + wn*WN + (lane%16)*FN + j]:
-    // for each (i, q) a lane holds FN consecutive columns of one row -> one vector store.  The output
-    // type is chosen once; each branch is straight-line code over the accumulators.
+    // Epilogue.  acc[i][j][q] = C[m0 + wm*WM + 16i + lane%16][n0 + wn*WN + 16j + 4*(lane/16) + q].
+    // The output type is chosen once; each branch is straight-line code over the accumulators.
     const size_t csz = dtype_size(d.dtype_c);
     char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
-    const int col0 = n0 + wn * C::WN + (lane & 15) * C::FN;
-    const int row0 = m0 + wm * C::WM + (lane >> 4) * 4 * C::FM;
-    const bool vec_ok = c_vec && col0 + C::FN <= d.N;
+    const int row0 = m0 + wm * C::WM + (lane & 15);
+    const int col0 = n0 + wn * C::WN + (lane >> 4) * 4;
+    const bool vec_ok = c_vec;
     if constexpr (__is_same(Acc, i32x4)) {
         if (d.dtype_c == TV_INT8) write_tile<int8_t, C>(acc, Cb, row0, col0, vec_ok, d);
         else write_tile<int32_t, C>(acc, Cb, row0, col0, vec_ok, d);
@@ -512,11 +519,9 @@ static int run_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
     if (nwg <= 0) return 0;
     if (nwg > 0x7FFFFFFF) return TV_E_SHAPE;
     const size_t csz = dtype_size(d.dtype_c);
-    // Vector stores of FN elements (aligned to FN elements, at most 16 bytes) along rows of C.
-    const int64_t fn = C::FN;
-    const size_t valign = fn * csz < 16 ? fn * csz : 16;
-    const int c_vec = d.sc_n == 1 && d.sc_m % fn == 0 && (d.batch <= 1 || d.sc_b % fn == 0) &&
-                      (reinterpret_cast<uintptr_t>(d.C) % valign) == 0;
+    // Vector stores of 4 elements (aligned to 4 elements) along rows of C.
+    const int c_vec = d.sc_n == 1 && d.sc_m % 4 == 0 && (d.batch <= 1 || d.sc_b % 4 == 0) &&
+                      (reinterpret_cast<uintptr_t>(d.C) % (4 * csz)) == 0;
     hipLaunchKernelGGL(gemm_mfma_kernel<C>, dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
                        group_m, c_vec);
     return hipGetLastError();
