@@ -319,6 +319,67 @@ __device__ inline void write_tile(const Acc (&acc)[C::FM][C::FN], char* Cb, int 
     }
 }
 
+// LDS bytes each wave gets for staging its output tile.
+constexpr int kEpiWaveBytes = 18432;
+
+// Staged store: the wave writes its accumulators (as TC) into its own LDS area, rows padded by 16
+// bytes (the 16 rows x 4 column groups of one write land on distinct banks), then copies them out
+// in 16-byte row chunks, so every global store covers whole row segments.  Rows are processed in
+// passes of RPP (all WM rows for 1- and 2-byte outputs).  Requires a contiguous row (sc_n == 1)
+// with 16-byte aligned row starts at the tile's column origin.
+template <typename TC, class C, typename Acc>
+__device__ inline void write_tile_staged(const Acc (&acc)[C::FM][C::FN], char* lds_wave, char* Cb, int lane, int mrow0,
+                                         int ncol0, const GemmDesc& d) {
+    constexpr int ROWB = C::WN * (int)sizeof(TC);            // bytes per output row of the wave tile
+    constexpr int PITCH = ROWB + 16;
+    constexpr int RPP0 = kEpiWaveBytes / PITCH / 16 * 16;
+    constexpr int RPP = RPP0 < C::WM ? RPP0 : C::WM;          // rows per pass
+    constexpr int CPR = ROWB / 16;                            // 16-byte chunks per row
+    static_assert(RPP >= 16 && C::WM % RPP == 0, "staging area too small");
+    typedef TC vec_t __attribute__((__vector_size__(4 * sizeof(TC))));
+#pragma unroll
+    for (int pass = 0; pass < C::WM / RPP; ++pass) {
+        // accumulators -> LDS: acc[i][j][q] is tile row 16i + lane%16, column 16j + 4*(lane/16) + q
+#pragma unroll
+        for (int i = pass * (RPP / 16); i < (pass + 1) * (RPP / 16); ++i) {
+            char* rowp = lds_wave + (16 * (i - pass * (RPP / 16)) + (lane & 15)) * PITCH + (lane >> 4) * 4 * sizeof(TC);
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) {
+                vec_t v;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = cvt_out<TC>(acc[i][j][q]);
+                *reinterpret_cast<vec_t*>(rowp + j * 16 * sizeof(TC)) = v;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        // LDS -> global, 16 bytes per lane, CPR lanes per row
+#pragma unroll
+        for (int idx = lane; idx < RPP * CPR; idx += 64) {
+            const int r = idx / CPR, c = idx % CPR;
+            const int row = mrow0 + pass * RPP + r;
+            const int col = ncol0 + c * (16 / (int)sizeof(TC));
+            if (row >= d.M) continue;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(lds_wave + r * PITCH + c * 16);
+            TC* dst = reinterpret_cast<TC*>(Cb) + (int64_t)row * d.sc_m + col;
+            if (col + 16 / (int)sizeof(TC) <= d.N) {
+                *reinterpret_cast<u32x4*>(dst) = v;
+            } else {
+                const TC* e = reinterpret_cast<const TC*>(&v);
+#pragma unroll
+                for (int q = 0; q < 16 / (int)sizeof(TC); ++q)
+                    if (col + q < d.N) dst[q] = e[q];
+            }
+        }
+        if (pass + 1 < C::WM / RPP) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        }
+    }
+}
+
 // Scheduling hints for the interleaved phases (LLVM AMDGPU sched_group_barrier masks).
 constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200, SG_VALU = 0x002;
 
@@ -341,7 +402,8 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
     using Acc = typename Op::Acc;
     constexpr int ES = C::ES;
 
-    __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+    constexpr int SMEM = 2 * C::STAGE > kEpiWaveBytes * C::THREADS / 64 ? 2 * C::STAGE : kEpiWaveBytes * C::THREADS / 64;
+    __shared__ __attribute__((aligned(16))) char smem[SMEM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -477,7 +539,22 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
     char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
     const int row0 = m0 + wm * C::WM + (lane & 15);
     const int col0 = n0 + wn * C::WN + (lane >> 4) * 4;
-    const bool vec_ok = c_vec;
+    const bool vec_ok = c_vec != 0;
+    if (c_vec == 2) {
+        // All waves are done with the k-loop's LDS stages before any wave reuses them.
+        lds_barrier();
+        char* lw = smem + wave * kEpiWaveBytes;
+        const int mrow0 = m0 + wm * C::WM, ncol0 = n0 + wn * C::WN;
+        if constexpr (__is_same(Acc, i32x4)) {
+            if (d.dtype_c == TV_INT8) write_tile_staged<int8_t, C>(acc, lw, Cb, lane, mrow0, ncol0, d);
+            else write_tile_staged<int32_t, C>(acc, lw, Cb, lane, mrow0, ncol0, d);
+        } else {
+            if (d.dtype_c == TV_BFLOAT16) write_tile_staged<__bf16, C>(acc, lw, Cb, lane, mrow0, ncol0, d);
+            else if (d.dtype_c == TV_FLOAT16) write_tile_staged<_Float16, C>(acc, lw, Cb, lane, mrow0, ncol0, d);
+            else write_tile_staged<float, C>(acc, lw, Cb, lane, mrow0, ncol0, d);
+        }
+        return;
+    }
     if constexpr (__is_same(Acc, i32x4)) {
         if (d.dtype_c == TV_INT8) write_tile<int8_t, C>(acc, Cb, row0, col0, vec_ok, d);
         else write_tile<int32_t, C>(acc, Cb, row0, col0, vec_ok, d);
@@ -519,9 +596,14 @@ static int run_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
     if (nwg <= 0) return 0;
     if (nwg > 0x7FFFFFFF) return TV_E_SHAPE;
     const size_t csz = dtype_size(d.dtype_c);
-    // Vector stores of 4 elements (aligned to 4 elements) along rows of C.
-    const int c_vec = d.sc_n == 1 && d.sc_m % 4 == 0 && (d.batch <= 1 || d.sc_b % 4 == 0) &&
-                      (reinterpret_cast<uintptr_t>(d.C) % (4 * csz)) == 0;
+    // c_vec = 1: 4-element vector stores along rows of C (aligned to 4 elements);
+    // c_vec = 2: LDS-staged 16-byte row chunks (rows 16-byte aligned at every tile origin).
+    int c_vec = d.sc_n == 1 && d.sc_m % 4 == 0 && (d.batch <= 1 || d.sc_b % 4 == 0) &&
+                (reinterpret_cast<uintptr_t>(d.C) % (4 * csz)) == 0;
+    const int64_t v16 = 16 / (int64_t)csz;
+    if (c_vec && d.sc_m % v16 == 0 && (d.batch <= 1 || d.sc_b % v16 == 0) &&
+        (reinterpret_cast<uintptr_t>(d.C) % 16) == 0 && (C::WN * (int64_t)csz) % 16 == 0)
+        c_vec = 2;
     hipLaunchKernelGGL(gemm_mfma_kernel<C>, dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
                        group_m, c_vec);
     return hipGetLastError();
