@@ -1,0 +1,79 @@
+// The HIP (MI355X) backend: context, storage and the matmul plugin, mirroring the reference's
+// CUDA backend interfaces (include/backend/cuda/cuda_context.h:8-68, cuda_tensor.h:12-47,
+// include/backend/cuda/ops/mul.h:6-15).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <memory>
+
+#include "context.h"
+#include "tensor.h"
+
+// One HIP device (the one with the most memory, as CUDAContext picks, cuda_context.h:14-36) and
+// one stream.  Ops enqueue on the stream and synchronise it before returning.
+class HIPContext : public ContextImpl {
+    int m_device_id = 0;
+    hipStream_t m_stream = nullptr;
+
+public:
+    HIPContext();
+    ~HIPContext() override;
+    void* ctx_raw_ptr() override { return &m_stream; }
+    hipStream_t stream() const { return m_stream; }
+    int device_id() const { return m_device_id; }
+    void wait() const;
+    // The process-wide context, created on first use (no GPU is touched at library load).
+    static std::shared_ptr<HIPContext> get();
+};
+
+// hipMalloc-backed storage (reference CUDATensor, include/backend/cuda/cuda_tensor.cpp:14-70).
+class HIPTensor : public TensorImpl {
+    size_t m_numel = 0;
+    via::DataType m_dtype = via::DataType::FLOAT32;
+    std::shared_ptr<HIPContext> m_context;
+    void* m_data = nullptr;
+
+public:
+    HIPTensor(void* host_ptr, size_t numel, via::DataType dtype, std::shared_ptr<HIPContext> ctx);
+    ~HIPTensor() override;
+    HIPTensor(const HIPTensor&) = delete;
+    HIPTensor& operator=(const HIPTensor&) = delete;
+    void* data() override { return m_data; }
+    const void* data() const override { return m_data; }
+    size_t numel() const override { return m_numel; }
+    void copy_to(std::shared_ptr<TensorImpl> dst) const override;
+    std::unique_ptr<TensorImpl> clone() const override;
+    std::unique_ptr<TensorImpl> clone_as_contiguous(const Metadata& meta) const override;
+    std::shared_ptr<ContextImpl> context() const override { return m_context; }
+    std::shared_ptr<HIPContext> hip_context() const { return m_context; }
+};
+
+// Host storage (reference CPUTensor, include/backend/cpu/cpu_tensor.cpp:9-69): the staging side
+// of to_host() / to_device().
+class CPUTensor : public TensorImpl {
+    size_t m_numel = 0;
+    via::DataType m_dtype = via::DataType::FLOAT32;
+    std::unique_ptr<char[]> m_data;
+
+public:
+    CPUTensor(void* ptr, size_t numel, via::DataType dtype);
+    void* data() override { return m_data.get(); }
+    const void* data() const override { return m_data.get(); }
+    size_t numel() const override { return m_numel; }
+    void copy_to(std::shared_ptr<TensorImpl> dst) const override;
+    std::unique_ptr<TensorImpl> clone() const override;
+    std::unique_ptr<TensorImpl> clone_as_contiguous(const Metadata& meta) const override;
+    std::shared_ptr<ContextImpl> context() const override { return nullptr; }
+};
+
+namespace ops {
+template <via::Device D> struct MulImpl;
+
+// The HIP matmul plugin: packs the two views into the C-ABI descriptor (include/tensorvia_hip.h)
+// and runs tv_hip_gemm on the context stream (replaces MulImpl<Device::CUDA>,
+// src/backend/cuda/mul.cu:52-124).
+template <> struct MulImpl<via::Device::HIP> {
+    static Tensor execute(const Tensor& a, const Tensor& b);
+};
+} // namespace ops

@@ -31,9 +31,10 @@
  *     SIMT kernel (slow path, provided for completeness).
  *
  * Calls are asynchronous on `hip_stream` (a hipStream_t, NULL = default stream).  The caller
- * keeps A, B and C alive until the stream has executed the work.  Calls that overlap on one
- * device share the library's GEMV reduction workspace only through per-call regions, so
- * concurrent streams are safe.
+ * keeps A, B and C alive until the stream has executed the work.  The split-K GEMV keeps its
+ * partial-sum workspace per (device, stream): calls on one stream are ordered by that stream, and
+ * calls on different streams use different workspaces, so concurrent streams are safe.  Growing
+ * a stream's workspace synchronises that stream once.
  */
 #ifndef TENSORVIA_HIP_H
 #define TENSORVIA_HIP_H
@@ -84,6 +85,23 @@ int tv_hip_gemm(const tv_gemm_args* args, void* hip_stream);
  * TV_E_UNSUPPORTED for M > 8 or for a dtype pair it does not serve. */
 int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream);
 
+/* Strided -> contiguous copy of one tensor view on the device (ndim <= TV_MAX_DIMS).  Element
+ * (i0, .., i{n-1}) of the view lives at src + sum_d i_d*strides[d] (element units, src already
+ * includes the view offset); dst receives the elements in row-major order.
+ * Replaces RepackImpl<Device::CUDA>::execute (reference src/backend/cuda/repack.cu:5-54), which
+ * backs TensorImpl::clone_as_contiguous (include/core/tensor.h:38) for Tensor::contiguous() /
+ * clone() of views (src/tensor.cpp:284-309). */
+#define TV_MAX_DIMS 8
+typedef struct tv_repack_args {
+    int32_t ndim;
+    int32_t elem_size;                 /* bytes per element: 1, 2, 4 or 8 */
+    int64_t shape[TV_MAX_DIMS];
+    int64_t strides[TV_MAX_DIMS];      /* element strides of the view */
+    const void* src;
+    void* dst;
+} tv_repack_args;
+int tv_hip_repack(const tv_repack_args* args, void* hip_stream);
+
 /* Human-readable text for any return code of this library. */
 const char* tv_hip_strerror(int code);
 
@@ -94,7 +112,7 @@ int tv_hip_abi_version(void);
  * the device.  Lets host code prove error propagation without a GPU.  count = 0 disarms. */
 void tv_hip_inject_fault(int code, int count);
 
-#define TV_HIP_ABI_VERSION 1
+#define TV_HIP_ABI_VERSION 2
 
 #ifdef __cplusplus
 }

@@ -27,7 +27,7 @@ TV_OK = 0
 TV_E_NULL, TV_E_SHAPE, TV_E_DTYPE, TV_E_UNSUPPORTED, TV_E_INJECTED, TV_E_NOMEM = -1, -2, -3, -4, -5, -6
 
 # Every symbol include/tensorvia_hip.h declares.
-EXPORTED_SYMBOLS = ("tv_hip_gemm", "tv_hip_gemv", "tv_hip_strerror", "tv_hip_abi_version",
+EXPORTED_SYMBOLS = ("tv_hip_gemm", "tv_hip_gemv", "tv_hip_repack", "tv_hip_strerror", "tv_hip_abi_version",
                     "tv_hip_inject_fault")
 
 
@@ -42,6 +42,17 @@ class TvGemmArgs(ctypes.Structure):
         ("B", ctypes.c_void_p), ("sb_b", ctypes.c_int64), ("sb_k", ctypes.c_int64), ("sb_n", ctypes.c_int64),
         ("C", ctypes.c_void_p), ("sc_b", ctypes.c_int64), ("sc_m", ctypes.c_int64), ("sc_n", ctypes.c_int64),
     ]
+
+
+TV_MAX_DIMS = 8
+
+
+class TvRepackArgs(ctypes.Structure):
+    """Mirror of ``tv_repack_args`` (include/tensorvia_hip.h)."""
+
+    _fields_ = [("ndim", ctypes.c_int32), ("elem_size", ctypes.c_int32),
+                ("shape", ctypes.c_int64 * TV_MAX_DIMS), ("strides", ctypes.c_int64 * TV_MAX_DIMS),
+                ("src", ctypes.c_void_p), ("dst", ctypes.c_void_p)]
 
 
 class TensorviaHipError(RuntimeError):
@@ -64,6 +75,8 @@ def lib() -> ctypes.CDLL:
         L.tv_hip_gemm.restype = ctypes.c_int
         L.tv_hip_gemv.argtypes = [ctypes.POINTER(TvGemmArgs), ctypes.c_void_p]
         L.tv_hip_gemv.restype = ctypes.c_int
+        L.tv_hip_repack.argtypes = [ctypes.POINTER(TvRepackArgs), ctypes.c_void_p]
+        L.tv_hip_repack.restype = ctypes.c_int
         L.tv_hip_strerror.argtypes = [ctypes.c_int]
         L.tv_hip_strerror.restype = ctypes.c_char_p
         L.tv_hip_abi_version.argtypes = []

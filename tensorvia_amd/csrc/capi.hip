@@ -119,6 +119,22 @@ int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream) {
     return tvk::launch_gemv(d, static_cast<hipStream_t>(hip_stream));
 }
 
+int tv_hip_repack(const tv_repack_args* args, void* hip_stream) {
+    int code;
+    if (take_fault(&code)) return code;
+    if (!args) return TV_E_NULL;
+    if (args->ndim < 0 || args->ndim > TV_MAX_DIMS) return TV_E_SHAPE;
+    if (args->elem_size != 1 && args->elem_size != 2 && args->elem_size != 4 && args->elem_size != 8) return TV_E_DTYPE;
+    int64_t n = 1;
+    for (int d = 0; d < args->ndim; ++d) {
+        if (args->shape[d] < 0) return TV_E_SHAPE;
+        n *= args->shape[d];
+    }
+    if (n == 0) return TV_OK;
+    if (!args->src || !args->dst) return TV_E_NULL;
+    return tvk::launch_repack(args, static_cast<hipStream_t>(hip_stream));
+}
+
 const char* tv_hip_strerror(int code) {
     switch (code) {
         case TV_OK: return "success";

@@ -41,6 +41,7 @@ enum LoadMode : int {
 // Launchers (return hipError_t, or a negative TV_E_* code).
 int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream);
 int launch_gemm_simt(const GemmDesc& d, hipStream_t stream);
+int launch_repack(const tv_repack_args* a, hipStream_t stream);
 int launch_gemv(const GemmDesc& d, hipStream_t stream); // TV_E_UNSUPPORTED if it does not serve d
 // GEMV with an explicit strip width (nl lanes), workgroup size and K split (tuning sweeps).
 int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices);

@@ -1,0 +1,223 @@
+// HIP backend: context, device/host storage, copies, registration and the matmul plugin.
+// Mirrors the reference CUDA backend's roles (include/backend/cuda/cuda_context.h:8-68,
+// cuda_tensor.cpp:14-70, cuda_copy.cpp:9-26, src/init.cpp:18-34, src/backend/cuda/mul.cu:52-124)
+// on the C-ABI of include/tensorvia_hip.h.
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "tensorvia/factory.h"
+#include "tensorvia/hip_backend.h"
+#include "tensorvia_hip.h"
+
+using namespace via;
+
+namespace {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void tv_check(int rc, const char* what) {
+    if (rc != TV_OK) throw std::runtime_error(std::string(what) + ": " + tv_hip_strerror(rc));
+}
+
+std::shared_ptr<HIPContext> hip_ctx_of(const std::shared_ptr<TensorImpl>& t) {
+    auto h = std::dynamic_pointer_cast<HIPTensor>(t);
+    if (!h) throw std::runtime_error("expected a HIP tensor");
+    return h->hip_context();
+}
+
+} // namespace
+
+// ---- HIPContext --------------------------------------------------------------------------------
+
+HIPContext::HIPContext() {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw std::runtime_error("No HIP devices found");
+    size_t best_mem = 0;
+    for (int i = 0; i < count; ++i) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, i) == hipSuccess && prop.totalGlobalMem > best_mem) {
+            best_mem = prop.totalGlobalMem;
+            m_device_id = i;
+        }
+    }
+    hip_check(hipSetDevice(m_device_id), "hipSetDevice");
+    hip_check(hipStreamCreate(&m_stream), "hipStreamCreate");
+}
+
+HIPContext::~HIPContext() {
+    if (m_stream) (void)hipStreamDestroy(m_stream);
+}
+
+void HIPContext::wait() const { hip_check(hipStreamSynchronize(m_stream), "hipStreamSynchronize"); }
+
+std::shared_ptr<HIPContext> HIPContext::get() {
+    static std::mutex mu;
+    static std::shared_ptr<HIPContext> ctx;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!ctx) ctx = std::make_shared<HIPContext>();
+    return ctx;
+}
+
+// ---- HIPTensor ---------------------------------------------------------------------------------
+
+HIPTensor::HIPTensor(void* host_ptr, size_t numel, DataType dtype, std::shared_ptr<HIPContext> ctx)
+    : m_numel(numel), m_dtype(dtype), m_context(std::move(ctx)) {
+    const size_t bytes = numel * calc_dtype_size(dtype);
+    hip_check(hipSetDevice(m_context->device_id()), "hipSetDevice");
+    hip_check(hipMalloc(&m_data, bytes), "hipMalloc");
+    if (host_ptr) {
+        hip_check(hipMemcpyAsync(m_data, host_ptr, bytes, hipMemcpyHostToDevice, m_context->stream()), "hipMemcpyAsync H2D");
+        m_context->wait();
+    }
+}
+
+HIPTensor::~HIPTensor() {
+    if (m_data) {
+        (void)hipStreamSynchronize(m_context->stream());
+        (void)hipFree(m_data);
+    }
+}
+
+void HIPTensor::copy_to(std::shared_ptr<TensorImpl> dst) const {
+    const size_t bytes = m_numel * calc_dtype_size(m_dtype);
+    hip_check(hipMemcpyAsync(dst->data(), m_data, bytes, hipMemcpyDeviceToDevice, m_context->stream()), "hipMemcpyAsync D2D");
+    m_context->wait();
+}
+
+std::unique_ptr<TensorImpl> HIPTensor::clone() const {
+    auto out = std::make_unique<HIPTensor>(nullptr, m_numel, m_dtype, m_context);
+    const size_t bytes = m_numel * calc_dtype_size(m_dtype);
+    hip_check(hipMemcpyAsync(out->data(), m_data, bytes, hipMemcpyDeviceToDevice, m_context->stream()), "hipMemcpyAsync D2D");
+    m_context->wait();
+    return out;
+}
+
+std::unique_ptr<TensorImpl> HIPTensor::clone_as_contiguous(const Metadata& meta) const {
+    auto out = std::make_unique<HIPTensor>(nullptr, meta.numel, m_dtype, m_context);
+    if (meta.shape.size() > TV_MAX_DIMS) throw std::runtime_error("clone_as_contiguous: too many dimensions");
+    tv_repack_args a{};
+    a.ndim = static_cast<int32_t>(meta.shape.size());
+    a.elem_size = static_cast<int32_t>(calc_dtype_size(m_dtype));
+    for (int d = 0; d < a.ndim; ++d) {
+        a.shape[d] = meta.shape[d];
+        a.strides[d] = meta.strides[d];
+    }
+    a.src = static_cast<const char*>(m_data) + meta.offset * a.elem_size;
+    a.dst = out->data();
+    tv_check(tv_hip_repack(&a, m_context->stream()), "tv_hip_repack");
+    m_context->wait();
+    return out;
+}
+
+// ---- CPUTensor ---------------------------------------------------------------------------------
+
+CPUTensor::CPUTensor(void* ptr, size_t numel, DataType dtype) : m_numel(numel), m_dtype(dtype) {
+    const size_t bytes = numel * calc_dtype_size(dtype);
+    m_data.reset(new char[bytes]);
+    if (ptr) std::memcpy(m_data.get(), ptr, bytes);
+}
+
+void CPUTensor::copy_to(std::shared_ptr<TensorImpl> dst) const {
+    std::memcpy(dst->data(), m_data.get(), m_numel * calc_dtype_size(m_dtype));
+}
+
+std::unique_ptr<TensorImpl> CPUTensor::clone() const {
+    return std::make_unique<CPUTensor>(m_data.get(), m_numel, m_dtype);
+}
+
+// Gather of a strided view into row-major order (reference include/backend/cpu/cpu_tensor.cpp:32-63).
+std::unique_ptr<TensorImpl> CPUTensor::clone_as_contiguous(const Metadata& meta) const {
+    auto out = std::make_unique<CPUTensor>(nullptr, meta.numel, m_dtype);
+    const size_t es = calc_dtype_size(m_dtype);
+    const char* src = m_data.get() + meta.offset * es;
+    char* dst = static_cast<char*>(out->data());
+    const size_t nd = meta.shape.size();
+    std::vector<int64_t> idx(nd, 0);
+    for (size_t i = 0; i < meta.numel; ++i) {
+        int64_t off = 0;
+        for (size_t d = 0; d < nd; ++d) off += idx[d] * meta.strides[d];
+        std::memcpy(dst + i * es, src + off * es, es);
+        for (size_t d = nd; d-- > 0;) {
+            if (++idx[d] < meta.shape[d]) break;
+            idx[d] = 0;
+        }
+    }
+    return out;
+}
+
+// ---- host <-> device ---------------------------------------------------------------------------
+
+void copy_device_to_host(std::shared_ptr<TensorImpl> src, std::shared_ptr<TensorImpl> dst, DataType dtype) {
+    auto ctx = hip_ctx_of(src);
+    // dst is sized to the tensor; src may be a larger storage whose leading elements are the tensor.
+    const size_t bytes = dst->numel() * calc_dtype_size(dtype);
+    hip_check(hipMemcpyAsync(dst->data(), src->data(), bytes, hipMemcpyDeviceToHost, ctx->stream()), "hipMemcpyAsync D2H");
+    ctx->wait();
+}
+
+void copy_host_to_device(std::shared_ptr<TensorImpl> src, std::shared_ptr<TensorImpl> dst, DataType dtype) {
+    auto ctx = hip_ctx_of(dst);
+    const size_t bytes = dst->numel() * calc_dtype_size(dtype);
+    hip_check(hipMemcpyAsync(dst->data(), src->data(), bytes, hipMemcpyHostToDevice, ctx->stream()), "hipMemcpyAsync H2D");
+    ctx->wait();
+}
+
+// ---- registration (no GPU is touched until the first HIP tensor) --------------------------------
+
+namespace {
+struct HIPRegistrar {
+    HIPRegistrar() {
+        register_tensor_impl(Device::HIP, [](void* ptr, size_t numel, DataType dtype) -> std::shared_ptr<TensorImpl> {
+            return std::make_shared<HIPTensor>(ptr, numel, dtype, HIPContext::get());
+        });
+        register_tensor_impl(Device::CPU, [](void* ptr, size_t numel, DataType dtype) -> std::shared_ptr<TensorImpl> {
+            return std::make_shared<CPUTensor>(ptr, numel, dtype);
+        });
+    }
+} hip_registrar;
+} // namespace
+
+// ---- MulImpl<HIP> ------------------------------------------------------------------------------
+
+namespace ops {
+
+Tensor MulImpl<Device::HIP>::execute(const Tensor& a, const Tensor& b) {
+    const bool a3 = a.dims() == 3, b3 = b.dims() == 3;
+    const int64_t batch = a3 ? a.shape(0) : 1;
+    const int64_t M = a.shape(-2), K = a.shape(-1), N = b.shape(-1);
+    const DataType res = compute_type(a.dtype(), b.dtype());
+    std::vector<int64_t> shape = a3 ? std::vector<int64_t>{batch, M, N} : std::vector<int64_t>{M, N};
+    Tensor c(shape, res, Device::HIP);
+
+    const std::vector<int64_t> sa = a.strides(), sb = b.strides(), sc = c.strides();
+    tv_gemm_args args{};
+    args.dtype_a = static_cast<int32_t>(a.dtype());
+    args.dtype_b = static_cast<int32_t>(b.dtype());
+    args.dtype_c = static_cast<int32_t>(res);
+    args.batch = batch;
+    args.M = M;
+    args.N = N;
+    args.K = K;
+    args.A = static_cast<const char*>(a.data()) + a.offset() * calc_dtype_size(a.dtype());
+    args.sa_b = a3 ? sa[0] : 0;
+    args.sa_m = sa[a3 ? 1 : 0];
+    args.sa_k = sa[a3 ? 2 : 1];
+    args.B = static_cast<const char*>(b.data()) + b.offset() * calc_dtype_size(b.dtype());
+    args.sb_b = b3 ? sb[0] : 0; // rank-2 B with rank-3 A: broadcast over the batch
+    args.sb_k = sb[b3 ? 1 : 0];
+    args.sb_n = sb[b3 ? 2 : 1];
+    args.C = c.data();
+    args.sc_b = a3 ? sc[0] : 0;
+    args.sc_m = sc[a3 ? 1 : 0];
+    args.sc_n = sc[a3 ? 2 : 1];
+
+    auto ctx = hip_ctx_of(c.get_impl());
+    tv_check(tv_hip_gemm(&args, ctx->stream()), "ops::Mul");
+    ctx->wait(); // the reference's op is synchronous (src/backend/cuda/mul.cu:122)
+    return c;
+}
+
+} // namespace ops

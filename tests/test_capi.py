@@ -40,16 +40,18 @@ def test_abi_version_matches_header():
     assert tv.lib().tv_hip_abi_version() == v
 
 
-def test_struct_layout_matches_c(tmp_path):
-    fields = [f for f, _ in TvGemmArgs._fields_]
+@pytest.mark.parametrize("struct,cname", [("TvGemmArgs", "tv_gemm_args"), ("TvRepackArgs", "tv_repack_args")])
+def test_struct_layout_matches_c(tmp_path, struct, cname):
+    S = getattr(tv, struct)
+    fields = [f for f, _ in S._fields_]
     src = tmp_path / "off.c"
     src.write_text("#include <stdio.h>\n#include <stddef.h>\n#include \"tensorvia_hip.h\"\nint main(void){\n"
-                   + "".join(f'printf("%zu\\n", offsetof(tv_gemm_args, {f}));\n' for f in fields)
-                   + 'printf("%zu\\n", sizeof(tv_gemm_args));return 0;}\n')
+                   + "".join(f'printf("%zu\\n", offsetof({cname}, {f}));\n' for f in fields)
+                   + f'printf("%zu\\n", sizeof({cname}));return 0;}}\n')
     exe = tmp_path / "off"
     subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
-    want = [getattr(TvGemmArgs, f).offset for f in fields] + [ctypes.sizeof(TvGemmArgs)]
+    want = [getattr(S, f).offset for f in fields] + [ctypes.sizeof(S)]
     assert got == want
 
 
