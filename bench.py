@@ -149,6 +149,28 @@ def run_gpu(name: str, steps: int, warmup: int):
     return res, inp
 
 
+def run_copy(steps: int, warmup: int) -> dict:
+    """Calibration for the HBM traffic counters: a plain device copy of a known size (512 MiB read,
+    512 MiB written per launch; larger than the 256 MB MALL)."""
+    import torch
+    n = 512 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    return {"workload": "device copy of 512 MiB (uint8)", "bytes_read": n, "bytes_written": n,
+            "kernel_ms_mean": ms, "hbm_gbs": 2 * n / (ms * 1e-3) / 1e9}
+
+
 def run_cpu(name: str, inp, iters: int):
     import oracle
     a, b, dt = inp["a"], inp["b"], inp["dt"]
@@ -164,10 +186,13 @@ def run_cpu(name: str, inp, iters: int):
         note = f"pre-materialised K^T (transpose {t_extra * 1e3:.1f} ms, excluded)"
     oracle.mul(a[:8], dt, b, dt) if a.ndim == 2 else None  # page in / thread pool warm-up
     times = []
-    for _ in range(iters):
+    t_start = time.perf_counter()
+    # At least `iters` calls, continuing until about 10 s of CPU time has been measured.
+    while len(times) < iters or (time.perf_counter() - t_start < 10.0 and len(times) < 50):
         t = time.perf_counter()
         oracle.mul(a, dt, b, dt)
         times.append(time.perf_counter() - t)
+    iters = len(times)
     flops, _ = work(name, inp)
     s = float(np.mean(times))
     return {"value": flops / s / 1e12, "unit": "TFLOP/s" if DTYPE[name] != "int8" else "TOP/s",
@@ -183,7 +208,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5m1,c5m8")
-    ap.add_argument("--only", default=None, help="run only this config's GPU kernel (for profilers)")
+    ap.add_argument("--only", default=None,
+                    help="run only this config's GPU kernel (for profilers); 'copy' runs the traffic calibration copy")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-all", action="store_true", help="CPU baseline for every config, not only c2")
     args = ap.parse_args()
@@ -200,6 +226,9 @@ def main() -> int:
     import tensorvia_amd as tv
     tv.lib()  # fail loudly if the kernel library is not built
 
+    if args.only == "copy":
+        print(json.dumps({"only": "copy", **run_copy(args.steps, args.warmup)}))
+        return 0
     names = [args.only] if args.only else args.configs.split(",")
     if "c2" not in names and not args.only:
         names.insert(0, "c2")
@@ -217,7 +246,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log("cpu baseline c2 (oracle)")
-        cpu = run_cpu("c2", inputs["c2"], iters=1)
+        cpu = run_cpu("c2", inputs["c2"], iters=3)
         log(f"cpu c2: {cpu['seconds']:.2f} s, {cpu['value'] * 1e3:.1f} GOP/s on {cpu['cores']} threads")
         if args.cpu_all:
             for n in names:
@@ -226,7 +255,7 @@ def main() -> int:
                     results[n]["cpu_baseline"] = run_cpu(n, inputs[n], iters=1)
 
     traffic = None
-    tf = ROOT / "profiles" / "c2_int8_gemm_traffic.json"
+    tf = ROOT / "profiles" / "gemm_int8_c2_traffic.json"
     if tf.exists():
         traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
     line = {
