@@ -109,18 +109,6 @@ template <int ES> __device__ inline unsigned load_bits(const char* p) {
 // K-contiguous LDS layout: row r holds 128 bytes of k; 16-byte chunk c is stored at c ^ ((r>>1)&7).
 __device__ inline int kc_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
-// A lane offset at or above 2^31 is outside every buffer resource built below (num_records <= 2^30),
-// also after a chunk's stride multiple (< 2^30) is added to it.
-constexpr unsigned kOOB = 0x80000000u;
-
-__device__ inline u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-}
-__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const char* base, int64_t bytes) {
-    const int nr = bytes <= 0 ? 0 : (bytes > 0x40000000 ? 0x40000000 : (int)bytes);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, nr, 0x00020000);
-}
-
 // Keeps the compiler from hoisting values derived from `v` out of a loop (they are cheaper to
 // recompute than to hold in registers across the MFMA loop).
 __device__ inline int opaque(int v) {

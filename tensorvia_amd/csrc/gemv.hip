@@ -1,100 +1,125 @@
 // Skinny-M (M <= 8) matmul for decode-shaped calls: x[b, M, K] @ W[b, K, N], W row-major
-// (N-contiguous).  HBM-bound: W is streamed exactly once with 16-byte loads and no matrix cores.
+// (N-contiguous).  HBM-bound: W is streamed exactly once with 16-byte buffer loads and no matrix
+// cores.
 //
 // The reference computes these shapes with mul_kernel_basic (src/backend/cpu/mul.cpp:7-25), chosen
 // because batch*M*N < 2^20 (mul.cpp:87-96), on one OpenMP thread when M = 1.
 //
-// Work split:
-//  * a workgroup owns a strip of NB = NL * VEC columns (NL lanes x 16 bytes of each W row) and, by
-//    default, the whole K range; its KL = THREADS / NL k-lanes walk contiguous row ranges;
-//  * narrow strips (64 bytes of a 128-byte line for bf16) give every CU a workgroup; workgroup ids
-//    are remapped so that neighbouring strips run on the same XCD and share W's lines in its L2;
-//  * each step reads VEC rows of W (VEC x 16 bytes per thread, double-buffered in registers) and
-//    one 16-byte chunk of x per row of x, which holds the same VEC k values;
-//  * products use the packed dot instructions: v_dot2_f32_bf16 / v_dot2_f32_f16 over pairs of
-//    rows, v_dot4_i32_i8 over quads of rows, plain fp32 FMA for fp32 — fp32 (int32) accumulation;
-//  * k-lanes are reduced with lane shuffles, then across waves through LDS, in a fixed order;
-//  * only when the strips cannot fill the GPU is K split over S workgroups: each writes its partial
-//    to a workspace and a second kernel sums the S partials in slice order (deterministic).  No
-//    cross-workgroup fences or atomics are used: an agent-scope release costs an L2 writeback per
-//    workgroup on this part.
+// Work split (measured on MI355X for W[4096, 11008] bf16; one CU alone streams only about
+// 29 GB/s, so W reaches HBM speed only when every CU streams, and partial 128-byte lines shared by
+// two workgroups cost more than they save):
+//  * a workgroup owns a strip of NB = NL * VEC columns (NL lanes x 16 bytes of each W row; 128-byte
+//    strips when N allows) and one K-slice; K is cut into S slices so that there are several
+//    hundred workgroups (W[4096, 11008]: 172 strips x 4 slices), which the dispatcher balances
+//    over the CUs;
+//  * the KL = THREADS / NL k-lanes of a workgroup take groups of GR = 4 consecutive rows in turn
+//    (group q goes to k-lane q mod KL), keeping DEPTH groups (16 loads) in flight per thread; loads
+//    past the end of the slice or right of column N use an out-of-range buffer offset and return
+//    zeros, so the loop has no branches;
+//  * x's slice is staged in LDS once per workgroup (while the first W loads are in flight);
+//  * products use the packed dot instructions over row pairs / quads of W, with the pairs built by
+//    v_perm_b32: v_dot2_f32_bf16 / v_dot2_f32_f16 (fp32 accumulation), v_dot4_i32_i8 (exact int32
+//    accumulation); fp32 uses fp32 FMA;
+//  * the k-lanes are summed through LDS in a fixed order;
+//  * with S > 1 each workgroup publishes its strip partial to slot s (agent-coherent stores) and
+//    counts itself in with an agent-scope atomic; the workgroup that arrives last sums slots
+//    0..S-1 in order (deterministic), writes C and resets the counter.  No workgroup waits for
+//    another, and there is no second kernel.
 #include "tv_kernels.h"
 
 namespace tvk {
 
 template <typename T> struct GemvTraits;
-template <> struct GemvTraits<float> { using Acc = float; static constexpr int P = 1; };
-template <> struct GemvTraits<__bf16> { using Acc = float; static constexpr int P = 2; };
-template <> struct GemvTraits<_Float16> { using Acc = float; static constexpr int P = 2; };
-template <> struct GemvTraits<int8_t> { using Acc = int; static constexpr int P = 4; };
+template <> struct GemvTraits<float> { using Acc = float; };
+template <> struct GemvTraits<__bf16> { using Acc = float; };
+template <> struct GemvTraits<_Float16> { using Acc = float; };
+template <> struct GemvTraits<int8_t> { using Acc = int; };
 
-// A workgroup owns NB = NL * VEC columns of W and one K-slice; NL lanes span the columns and
-// KL = THREADS / NL "k-lanes" walk contiguous row ranges of the slice.
+constexpr int kGemvThreads = 256;
+constexpr int kGemvGroupRows = 4;  // GR
+constexpr int kGemvDepth = 4;      // groups in flight per thread
+constexpr int kGemvXBytes = 65536; // LDS for x's slice at MR = 8
+constexpr int kGemvMaxSlices = 16; // K slices combined in-kernel
+
+// Rows of x staged per slice: MR * kslice * sizeof(T) <= kGemvXBytes at MR = 8.
+template <typename T> constexpr int gemv_kcap() { return kGemvXBytes / (8 * (int)sizeof(T)); }
+
 struct GemvArgs {
     GemmDesc d;
-    int kslice;      // rows per K-slice (a multiple of KL * VEC)
-    int nslices;     // S: K-slices; S > 1 writes partials for gemv_reduce_kernel
-    int nblk;        // column blocks per batch
-    void* ws;        // [S][batch][MR][N] partials (S > 1)
+    int kslice;  // rows per K-slice (a multiple of VEC, at most gemv_kcap<T>())
+    int nslices; // S
+    int nblk;    // strips per batch
+    int* cnt;    // [batch * nblk] arrival counters (S > 1), zero between launches
+    void* part;  // [batch * nblk][S][MR][NB] strip partials (S > 1)
 };
 
-// Accumulate VEC rows (one 16-byte W chunk per row) against the matching x chunks.
 template <typename T, int MR>
-__device__ inline void gemv_step(const u32x4 (&w)[16 / sizeof(T)], const u32x4 (&x)[MR],
-                                 typename GemvTraits<T>::Acc (&acc)[MR][16 / sizeof(T)]) {
+__device__ inline void gemv_group(const u32x4 (&w)[kGemvGroupRows], const char* xs, int xstride,
+                                  typename GemvTraits<T>::Acc (&acc)[MR][16 / sizeof(T)]) {
     constexpr int VEC = 16 / sizeof(T);
     if constexpr (sizeof(T) == 4) {
-        // Whole-vector casts: clang's __builtin_bit_cast of a vector *element* reads element 0.
 #pragma unroll
-        for (int r = 0; r < VEC; ++r) {
-            const f32x4 wf = __builtin_bit_cast(f32x4, w[r]);
+        for (int m = 0; m < MR; ++m) {
+            const f32x4 xv = *reinterpret_cast<const f32x4*>(xs + m * xstride);
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const float xv = __builtin_bit_cast(f32x4, x[m])[r];
+            for (int r = 0; r < kGemvGroupRows; ++r) {
+                const f32x4 wf = __builtin_bit_cast(f32x4, w[r]);
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) acc[m][e] = __builtin_fmaf(xv, wf[e], acc[m][e]);
+                for (int e = 0; e < VEC; ++e) acc[m][e] = __builtin_fmaf(xv[r], wf[e], acc[m][e]);
             }
         }
     } else if constexpr (sizeof(T) == 2) {
+        // pair p = rows (2p, 2p+1); dword t of a row holds columns 2t, 2t+1
+        unsigned lo[2][4], hi[2][4];
 #pragma unroll
-        for (int r = 0; r < VEC; r += 2) {
-            unsigned wp[VEC];
+        for (int p = 0; p < 2; ++p)
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                const unsigned lo = (w[r][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-                const unsigned hi = (w[r + 1][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-                wp[e] = lo | (hi << 16);
+            for (int t = 0; t < 4; ++t) {
+                lo[p][t] = __builtin_amdgcn_perm(w[2 * p + 1][t], w[2 * p][t], 0x05040100u);
+                hi[p][t] = __builtin_amdgcn_perm(w[2 * p + 1][t], w[2 * p][t], 0x07060302u);
             }
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const unsigned xp = x[m][r >> 1];
+        for (int m = 0; m < MR; ++m) {
+            // x rows (0,1) and (2,3) as two scalars: clang's __builtin_bit_cast of a vector
+            // *element* reads element 0, so no vector type is indexed here.
+            const unsigned* xr = reinterpret_cast<const unsigned*>(xs + m * xstride);
+            const unsigned xp[2] = {xr[0], xr[1]};
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    if constexpr (__is_same(T, __bf16))
-                        acc[m][e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xp),
-                                                                    __builtin_bit_cast(bf16x2, wp[e]), acc[m][e], false);
-                    else
-                        acc[m][e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, xp),
-                                                           __builtin_bit_cast(f16x2, wp[e]), acc[m][e], false);
+            for (int p = 0; p < 2; ++p)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    if constexpr (__is_same(T, __bf16)) {
+                        acc[m][2 * t] = __builtin_amdgcn_fdot2_f32_bf16(
+                            __builtin_bit_cast(bf16x2, xp[p]), __builtin_bit_cast(bf16x2, lo[p][t]), acc[m][2 * t], false);
+                        acc[m][2 * t + 1] = __builtin_amdgcn_fdot2_f32_bf16(
+                            __builtin_bit_cast(bf16x2, xp[p]), __builtin_bit_cast(bf16x2, hi[p][t]), acc[m][2 * t + 1], false);
+                    } else {
+                        acc[m][2 * t] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, xp[p]),
+                                                               __builtin_bit_cast(f16x2, lo[p][t]), acc[m][2 * t], false);
+                        acc[m][2 * t + 1] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, xp[p]),
+                                                                   __builtin_bit_cast(f16x2, hi[p][t]), acc[m][2 * t + 1], false);
+                    }
                 }
-            }
         }
     } else {
+        // the four rows' bytes of column c gathered into one dword (row r in byte r)
+        unsigned q[16];
 #pragma unroll
-        for (int r = 0; r < VEC; r += 4) {
-            unsigned wq[VEC];
+        for (int t = 0; t < 4; ++t) {
+            const unsigned a01l = __builtin_amdgcn_perm(w[1][t], w[0][t], 0x05010400u); // r0.b0 r1.b0 r0.b1 r1.b1
+            const unsigned a01h = __builtin_amdgcn_perm(w[1][t], w[0][t], 0x07030602u); // r0.b2 r1.b2 r0.b3 r1.b3
+            const unsigned a23l = __builtin_amdgcn_perm(w[3][t], w[2][t], 0x05010400u);
+            const unsigned a23h = __builtin_amdgcn_perm(w[3][t], w[2][t], 0x07030602u);
+            q[4 * t + 0] = __builtin_amdgcn_perm(a23l, a01l, 0x05040100u);
+            q[4 * t + 1] = __builtin_amdgcn_perm(a23l, a01l, 0x07060302u);
+            q[4 * t + 2] = __builtin_amdgcn_perm(a23h, a01h, 0x05040100u);
+            q[4 * t + 3] = __builtin_amdgcn_perm(a23h, a01h, 0x07060302u);
+        }
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                const int sh = 8 * (e & 3), dw = e >> 2;
-                wq[e] = ((w[r][dw] >> sh) & 0xFFu) | (((w[r + 1][dw] >> sh) & 0xFFu) << 8) |
-                        (((w[r + 2][dw] >> sh) & 0xFFu) << 16) | (((w[r + 3][dw] >> sh) & 0xFFu) << 24);
-            }
+        for (int m = 0; m < MR; ++m) {
+            const int xq = *reinterpret_cast<const int*>(xs + m * xstride);
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const int xq = (int)x[m][r >> 2];
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) acc[m][e] = __builtin_amdgcn_sdot4(xq, (int)wq[e], acc[m][e], false);
-            }
+            for (int e = 0; e < 16; ++e) acc[m][e] = __builtin_amdgcn_sdot4(xq, (int)q[e], acc[m][e], false);
         }
     }
 }
@@ -111,25 +136,34 @@ __device__ inline void gemv_store(void* C, int64_t idx, int dtype_c, Acc v) {
     }
 }
 
-// Workgroup ids are remapped so that neighbouring column blocks (which share 128-byte lines of W
-// when NB * sizeof(T) < 128) run on the same XCD and meet in its L2.
+// Workgroup ids are remapped so that neighbouring column strips (which share 128-byte lines of W)
+// run on the same XCD and meet in its L2 (workgroups are dealt round-robin over the 8 XCDs).
 __device__ inline int xcd_remap(int bid, int nwg) {
     return (nwg & 7) == 0 ? (bid & 7) * (nwg >> 3) + (bid >> 3) : bid;
 }
 
+template <typename T, int MR, int NL, int THREADS> struct GemvShape {
+    static constexpr int ES = sizeof(T);
+    static constexpr int VEC = 16 / ES;
+    static constexpr int NB = NL * VEC;     // columns per strip
+    static constexpr int KL = THREADS / NL; // k-lanes
+    static constexpr int P = KL / VEC;      // threads that sum one output
+    static constexpr int KCAP = gemv_kcap<T>();
+    static_assert(P >= 1 && 64 % P == 0 && P * NB == THREADS, "reduction lanes");
+};
+
 template <typename T, int MR, int NL, int THREADS>
-__global__ __launch_bounds__(THREADS) void gemv_ncontig_kernel(GemvArgs g) {
+__global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
     using Acc = typename GemvTraits<T>::Acc;
-    constexpr int ES = sizeof(T);
-    constexpr int VEC = 16 / ES;
-    constexpr int NB = NL * VEC;
-    constexpr int KL = THREADS / NL;
-    constexpr int NWAVES = THREADS / 64;
-    constexpr int LPW = 64 / NL; // k-lanes per wave
-    static_assert(64 % NL == 0 && THREADS % 64 == 0, "n-lanes must tile a wave");
+    using S = GemvShape<T, MR, NL, THREADS>;
+    constexpr int ES = S::ES, VEC = S::VEC, NB = S::NB, KL = S::KL, P = S::P;
+    constexpr int GR = kGemvGroupRows, DEPTH = kGemvDepth;
+    static_assert(64 % NL == 0, "n-lanes must tile a wave");
     const GemmDesc& d = g.d;
 
-    __shared__ Acc part[NWAVES][MR][NB];
+    extern __shared__ __attribute__((aligned(16))) char xs[]; // MR * kslice * ES bytes (launch size)
+    __shared__ Acc red[NB * (KL + 1)];
+    __shared__ int last_flag;
 
     const int tid = threadIdx.x;
     const int nl = tid % NL, kl = tid / NL;
@@ -140,14 +174,40 @@ __global__ __launch_bounds__(THREADS) void gemv_ncontig_kernel(GemvArgs g) {
     const int col = n0 + nl * VEC;
     const bool col_ok = col < d.N; // N % VEC == 0 is a launch precondition
 
-    const int kbeg_slice = s * g.kslice;
-    const int kend_slice = min(d.K, kbeg_slice + g.kslice);
-    const int per_lane = g.kslice / KL; // multiple of VEC
-    const int kbeg = kbeg_slice + kl * per_lane;
-    const int kend = min(kend_slice, kbeg + per_lane);
+    const int k0 = s * g.kslice;
+    const int ks = min(d.K - k0, g.kslice); // rows of this slice, a multiple of GR
+    const int ngroups = ks / GR;
+    const int niter = (ngroups + KL - 1) / KL;
 
-    const char* W = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + col) * ES;
-    const char* X = static_cast<const char*>(d.A) + (int64_t)b * d.sa_b * ES;
+    // W rows [k0, k0 + ks) of batch b; row r of the slice, this lane's columns at r * rowb + colb.
+    const int64_t rowb = d.sb_k * ES;
+    const char* wbase = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)k0 * d.sb_k) * ES;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wbase, (int64_t)(ks - 1) * rowb + (int64_t)d.N * ES);
+    const unsigned colb = (unsigned)(col * ES);
+
+    u32x4 w[DEPTH][GR];
+    auto issue = [&](int slot, int j) {
+        const int q = kl + j * KL;
+        const bool ok = col_ok && q < ngroups;
+        const unsigned base = (unsigned)(q * GR * rowb) + colb;
+#pragma unroll
+        for (int r = 0; r < GR; ++r) w[slot][r] = buf_load16_nt(wr, ok ? base + (unsigned)(r * rowb) : kOOB);
+    };
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) issue(j, j);
+
+    // Stage x[b][0..MR)[k0 .. k0 + ks) in LDS (rows m >= M are zero).
+    {
+        const char* xb = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + k0) * ES;
+        const int cpr = ks * ES / 16; // 16-byte chunks per row
+        for (int i = tid; i < MR * cpr; i += THREADS) {
+            const int m = i / cpr, c = i - m * cpr;
+            u32x4 v = {0, 0, 0, 0};
+            if (m < d.M) v = *reinterpret_cast<const u32x4*>(xb + (int64_t)m * d.sa_m * ES + c * 16);
+            *reinterpret_cast<u32x4*>(xs + m * ks * ES + c * 16) = v;
+        }
+    }
+    __syncthreads();
 
     Acc acc[MR][VEC];
 #pragma unroll
@@ -155,94 +215,87 @@ __global__ __launch_bounds__(THREADS) void gemv_ncontig_kernel(GemvArgs g) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[m][e] = 0;
 
-    auto load_w = [&](int k, u32x4 (&w)[VEC]) {
+    const int xstride = ks * ES;
+    for (int j0 = 0; j0 < niter; j0 += DEPTH) {
 #pragma unroll
-        for (int r = 0; r < VEC; ++r) {
-            if (col_ok && k + r < kend)
-                w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W + (int64_t)(k + r) * d.sb_k * ES));
-            else
-                w[r] = u32x4{0, 0, 0, 0};
-        }
-    };
-    auto load_x = [&](int k, u32x4 (&x)[MR]) {
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            if (m < d.M && k < kend)
-                x[m] = *reinterpret_cast<const u32x4*>(X + ((int64_t)m * d.sa_m + k) * ES);
-            else
-                x[m] = u32x4{0, 0, 0, 0};
-        }
-    };
-
-    if (kbeg < kend) {
-        u32x4 w0[VEC], w1[VEC], x0[MR], x1[MR];
-        load_w(kbeg, w0);
-        load_x(kbeg, x0);
-        int k = kbeg;
-        for (; k + VEC < kend; k += 2 * VEC) {
-            load_w(k + VEC, w1);
-            load_x(k + VEC, x1);
-            gemv_step<T, MR>(w0, x0, acc);
-            if (k + 2 * VEC < kend) {
-                load_w(k + 2 * VEC, w0);
-                load_x(k + 2 * VEC, x0);
+        for (int dd = 0; dd < DEPTH; ++dd) {
+            const int j = j0 + dd;
+            if (j < niter) {
+                int q = kl + j * KL;
+                q = q < ngroups ? q : 0; // past the end: w is zero, keep the x read in range
+                gemv_group<T, MR>(w[dd], xs + q * GR * ES, xstride, acc);
+                if (j + DEPTH < niter) issue(dd, j + DEPTH);
             }
-            gemv_step<T, MR>(w1, x1, acc);
         }
-        if (k < kend) gemv_step<T, MR>(w0, x0, acc);
     }
 
-    // Reduce the LPW k-lanes of each wave (lanes nl + NL*j), then the waves through LDS.
-    const int wave = tid >> 6, lane = tid & 63;
+    // Sum the k-lanes one row of x at a time: red[c * (KL + 1) + kl]; output c is summed by the P
+    // consecutive threads c * P .. c * P + P - 1 (VEC partials each, in k-lane order), then a fixed
+    // shuffle tree.  Thread c * P keeps the strip's result for row m in v[m].
+    const int oc = tid / P, part = tid % P;
+    Acc v[MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
+    for (int m = 0; m < MR; ++m) {
+        v[m] = 0;
+        if (m >= d.M) break;
+        __syncthreads();
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            Acc v = acc[m][e];
+        for (int e = 0; e < VEC; ++e) red[(nl * VEC + e) * (KL + 1) + kl] = acc[m][e];
+        __syncthreads();
+        const Acc* p = red + oc * (KL + 1) + part * VEC;
+        Acc t = p[0];
 #pragma unroll
-            for (int off = NL; off < 64; off <<= 1) v += __shfl_xor(v, off);
-            acc[m][e] = v;
-        }
-    (void)LPW;
-    if (lane < NL) {
+        for (int i = 1; i < VEC; ++i) t += p[i];
 #pragma unroll
-        for (int m = 0; m < MR; ++m)
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) part[wave][m][lane * VEC + e] = acc[m][e];
+        for (int off = 1; off < P; off <<= 1) t += __shfl_xor(t, off);
+        v[m] = t;
     }
-    __syncthreads();
 
     const size_t csz = dtype_size(d.dtype_c);
     char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
-    Acc* ws = g.nslices > 1 ? static_cast<Acc*>(g.ws) + (((int64_t)s * d.batch + b) * MR) * d.N : nullptr;
-    for (int i = tid; i < MR * NB; i += THREADS) {
-        const int m = i / NB, c = i % NB;
-        if (m < d.M && n0 + c < d.N) {
-            Acc v = part[0][m][c];
+    const bool writer = part == 0 && n0 + oc < d.N;
+    if (g.nslices == 1) {
+        if (writer)
 #pragma unroll
-            for (int w = 1; w < NWAVES; ++w) v += part[w][m][c];
-            if (ws) ws[(int64_t)m * d.N + n0 + c] = v;
-            else gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + c) * d.sc_n, d.dtype_c, v);
+            for (int m = 0; m < MR; ++m)
+                if (m < d.M) gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + oc) * d.sc_n, d.dtype_c, v[m]);
+        return;
+    }
+
+    // Publish slot s of this strip, count in; the last arriver sums the slots in order.
+    const int strip = lin;
+    Acc* slots = static_cast<Acc*>(g.part) + (int64_t)strip * g.nslices * MR * NB;
+    if (part == 0)
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+            if (m < d.M) __hip_atomic_store(slots + ((int64_t)s * MR + m) * NB + oc, v[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads(); // every partial store of this workgroup has completed (s_waitcnt before s_barrier)
+    if (tid == 0)
+        last_flag = __hip_atomic_fetch_add(g.cnt + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g.nslices - 1;
+    __syncthreads();
+    if (!last_flag) return;
+    for (int o = tid; o < MR * NB; o += THREADS) {
+        const int m = o / NB, c = o - m * NB;
+        if (m < d.M && n0 + c < d.N) {
+            // All slot loads are issued before the first add (S <= kGemvMaxSlices).
+            Acc part_v[kGemvMaxSlices];
+#pragma unroll
+            for (int k = 0; k < kGemvMaxSlices; ++k)
+                part_v[k] = k < g.nslices ? __hip_atomic_load(slots + ((int64_t)k * MR + m) * NB + c, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT)
+                                          : Acc(0);
+            Acc t = part_v[0];
+#pragma unroll
+            for (int k = 1; k < kGemvMaxSlices; ++k)
+                if (k < g.nslices) t += part_v[k];
+            gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + c) * d.sc_n, d.dtype_c, t);
         }
     }
+    if (tid == 0) __hip_atomic_store(g.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Split-K epilogue: C[b, m, n] = sum over slices s = 0..S-1, in slice order (deterministic).
-template <typename Acc>
-__global__ __launch_bounds__(256) void gemv_reduce_kernel(GemvArgs g, int mr) {
-    const GemmDesc& d = g.d;
-    const int64_t total = (int64_t)d.batch * d.M * d.N;
-    const int64_t stride_s = (int64_t)d.batch * mr * d.N;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t n = i % d.N;
-        const int64_t m = (i / d.N) % d.M;
-        const int64_t b = i / ((int64_t)d.N * d.M);
-        const Acc* p = static_cast<const Acc*>(g.ws) + (b * mr + m) * d.N + n;
-        Acc v = 0;
-        for (int s = 0; s < g.nslices; ++s) v += p[s * stride_s];
-        const size_t csz = dtype_size(d.dtype_c);
-        gemv_store(static_cast<char*>(d.C) + b * d.sc_b * csz, m * d.sc_m + n * d.sc_n, d.dtype_c, v);
-    }
+__global__ __launch_bounds__(256) void gemv_zero_kernel(int* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -251,24 +304,27 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(GemvArgs g, int mr) {
 
 #include <map>
 #include <mutex>
+#include <tuple>
 
 namespace tvk {
 
-// Per-(device, stream) workspace for split-K partials.  Calls on one stream are ordered by the
-// stream, so they can share it.
+// Per-(device, stream, kind) workspace.  Calls on one stream are ordered by the stream, so they
+// can share it.
 struct GemvWorkspace {
     void* base = nullptr;
     size_t bytes = 0;
 };
 static std::mutex g_ws_mu;
-static std::map<std::pair<int, hipStream_t>, GemvWorkspace> g_ws;
+static std::map<std::tuple<int, hipStream_t, int>, GemvWorkspace> g_ws;
 
-static int get_workspace(hipStream_t stream, size_t need, void** out) {
+// kind 1: the split-K arrival counters (only gemv_kernel writes them, and every launch leaves them
+// at zero); kind 2: the strip partial slots.
+static int get_workspace(hipStream_t stream, size_t need, void** out, int kind) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    GemvWorkspace& w = g_ws[{dev, stream}];
+    GemvWorkspace& w = g_ws[{dev, stream, kind}];
     if (w.bytes < need) {
         if (w.base) {
             // The old buffer may still be in use by queued work of this stream.
@@ -282,6 +338,12 @@ static int get_workspace(hipStream_t stream, size_t need, void** out) {
         e = hipMalloc(&w.base, sz);
         if (e != hipSuccess) return TV_E_NOMEM;
         w.bytes = sz;
+        // The arrival counters must start at zero (each launch leaves them at zero again).  A fill
+        // kernel rather than a memset node, for callers that capture.
+        hipLaunchKernelGGL(gemv_zero_kernel, dim3(256), dim3(256), 0, stream, static_cast<int*>(w.base),
+                           (int64_t)(sz / sizeof(int)));
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
     *out = w.base;
     return 0;
@@ -290,12 +352,14 @@ static int get_workspace(hipStream_t stream, size_t need, void** out) {
 // Whether the vectorised GEMV serves this call.
 static bool gemv_layout_ok(const GemmDesc& d) {
     if (d.dtype_a != d.dtype_b) return false;
+    if (d.dtype_a != TV_FLOAT32 && d.dtype_a != TV_BFLOAT16 && d.dtype_a != TV_FLOAT16 && d.dtype_a != TV_INT8) return false;
     const int es = (int)dtype_size(d.dtype_a);
     const int64_t vec = 16 / es;
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     if (d.M < 1 || d.M > 8) return false;
     if (d.sb_n != 1 || !al(d.B) || d.N % vec || (d.K > 1 && d.sb_k % vec) || (d.batch > 1 && d.sb_b % vec)) return false;
     if (d.sa_k != 1 || !al(d.A) || d.K % vec || (d.M > 1 && d.sa_m % vec) || (d.batch > 1 && d.sa_b % vec)) return false;
+    if (d.K > 1 && d.sb_k < d.N) return false;
     return true;
 }
 
@@ -303,75 +367,92 @@ struct GemvPlan {
     int nl, threads, nslices;
 };
 
-// Column strip width and K split (measured on MI355X for x[1|8,4096] @ W[4096,11008] bf16):
-// 128-byte strips (NL = 8) over the whole K with 512 threads stream W best for M <= 2; wider
-// strips with a 2-way K split suit M > 2, whose 8 accumulator rows limit occupancy.  K is split
-// further only when the strips cannot give every CU a workgroup.
+// Strip width: 128 bytes (8 lanes) unless N has fewer 16-byte chunks.
+static int gemv_nl(const GemmDesc& d) {
+    const int nch = d.N / (16 / (int)dtype_size(d.dtype_a));
+    return nch >= 8 ? 8 : (nch >= 4 ? 4 : 2);
+}
+
+// K slices: enough for about 1376 workgroups in all at M <= 2 and 344 above (W[4096, 11008] bf16:
+// 172 strips x 8 or x 2, measured best; larger M has a longer per-workgroup reduction), at least what
+// x's LDS slice needs, and no more than leaves every k-lane two row groups per slice.
 static GemvPlan gemv_plan(const GemmDesc& d) {
+    const int nl = gemv_nl(d);
     const int vec = 16 / (int)dtype_size(d.dtype_a);
-    GemvPlan p = d.M <= 2 ? GemvPlan{8, 512, 1} : GemvPlan{16, 256, 2};
-    const int64_t nblk = ((int64_t)d.N + p.nl * vec - 1) / (p.nl * vec) * d.batch;
-    const int unit = (p.threads / p.nl) * vec;
-    const int max_s = (d.K + 2 * unit - 1) / (2 * unit);
-    int s = p.nslices;
-    if (nblk * s < 128) s = (int)((256 + nblk - 1) / nblk);
-    p.nslices = s < max_s ? s : max_s;
-    if (p.nslices < 1) p.nslices = 1;
-    return p;
+    const int64_t strips = (d.N / vec + nl - 1) / nl * (int64_t)d.batch;
+    const int kcap = kGemvXBytes / (8 * (int)dtype_size(d.dtype_a));
+    const int min_s = (d.K + kcap - 1) / kcap;
+    const int rows_min = 2 * kGemvGroupRows * (kGemvThreads / nl);
+    const int max_s = d.K / rows_min > 1 ? d.K / rows_min : 1;
+    const int64_t target = d.M <= 2 ? 1376 : 344;
+    int s = (int)((target + strips - 1) / strips);
+    if (s > max_s) s = max_s;
+    if (s > kGemvMaxSlices) s = kGemvMaxSlices;
+    if (s < min_s) s = min_s;
+    return GemvPlan{nl, kGemvThreads, s < 1 ? 1 : s};
 }
 
 template <typename T, int MR, int NL, int THREADS>
 static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices) {
-    constexpr int VEC = 16 / sizeof(T);
-    constexpr int NB = NL * VEC;
-    constexpr int KL = THREADS / NL;
+    using Sh = GemvShape<T, MR, NL, THREADS>;
     using Acc = typename GemvTraits<T>::Acc;
-    const int nblk = (d.N + NB - 1) / NB;
-    const int unit = KL * VEC;
+    const int vec = Sh::VEC;
+    const int nblk = (d.N + Sh::NB - 1) / Sh::NB;
     int S = nslices < 1 ? 1 : nslices;
+    const int min_s = (d.K + Sh::KCAP - 1) / Sh::KCAP;
+    if (S < min_s) S = min_s;
     int kslice = (d.K + S - 1) / S;
-    kslice = (kslice + unit - 1) / unit * unit;
-    if (kslice < unit) kslice = unit;
+    kslice = (kslice + vec - 1) / vec * vec;
+    if (kslice > Sh::KCAP) kslice = Sh::KCAP; // KCAP is a multiple of every VEC
     S = (d.K + kslice - 1) / kslice;
-    if (S < 1) S = 1;
+    if (S > kGemvMaxSlices) return TV_E_UNSUPPORTED; // K beyond 16 LDS slices: the GEMM path serves it
+    // Buffer offsets of one slice stay below 2^30.
+    if ((int64_t)(kslice - 1) * d.sb_k * Sh::ES + (int64_t)d.N * Sh::ES >= ((int64_t)1 << 30)) return TV_E_UNSUPPORTED;
+    const int64_t nwg = (int64_t)nblk * d.batch;
+    if (nwg > 0x7FFFFFFF || S > 65535) return TV_E_SHAPE;
 
     GemvArgs g;
     g.d = d;
     g.kslice = kslice;
     g.nslices = S;
     g.nblk = nblk;
-    g.ws = nullptr;
+    g.cnt = nullptr;
+    g.part = nullptr;
     if (S > 1) {
-        int rc = get_workspace(stream, (size_t)S * d.batch * MR * d.N * sizeof(Acc), &g.ws);
+        void* cnt = nullptr;
+        int rc = get_workspace(stream, (size_t)nwg * sizeof(int), &cnt, 1);
         if (rc) return rc;
+        rc = get_workspace(stream, (size_t)nwg * S * MR * Sh::NB * sizeof(Acc), &g.part, 2);
+        if (rc) return rc;
+        g.cnt = static_cast<int*>(cnt);
     }
-    const int64_t nwg = (int64_t)nblk * d.batch;
-    if (nwg > 0x7FFFFFFF) return TV_E_SHAPE;
-    hipLaunchKernelGGL((gemv_ncontig_kernel<T, MR, NL, THREADS>), dim3((unsigned)nwg, S), dim3(THREADS), 0, stream, g);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || S == 1) return e;
-    const int64_t total = (int64_t)d.batch * d.M * d.N;
-    int64_t blocks = (total + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL((gemv_reduce_kernel<Acc>), dim3((unsigned)blocks), dim3(256), 0, stream, g, MR);
+    hipLaunchKernelGGL((gemv_kernel<T, MR, NL, THREADS>), dim3((unsigned)nwg, S), dim3(THREADS),
+                       (size_t)MR * kslice * Sh::ES, stream, g);
     return hipGetLastError();
 }
 
 template <typename T, int MR>
-static int gemv_dispatch_cfg(const GemmDesc& d, hipStream_t stream, const GemvPlan& p) {
-    if (p.nl == 4 && p.threads == 256) return gemv_run<T, MR, 4, 256>(d, stream, p.nslices);
-    if (p.nl == 8 && p.threads == 512) return gemv_run<T, MR, 8, 512>(d, stream, p.nslices);
-    if (p.nl == 8 && p.threads == 1024) return gemv_run<T, MR, 8, 1024>(d, stream, p.nslices);
-    if (p.nl == 16 && p.threads == 256) return gemv_run<T, MR, 16, 256>(d, stream, p.nslices);
+static int gemv_dispatch_nl(const GemmDesc& d, hipStream_t stream, const GemvPlan& p) {
+    if (p.threads == 256) {
+        switch (p.nl) {
+            case 2: return gemv_run<T, MR, 2, 256>(d, stream, p.nslices);
+            case 4: return gemv_run<T, MR, 4, 256>(d, stream, p.nslices);
+            case 8: return gemv_run<T, MR, 8, 256>(d, stream, p.nslices);
+        }
+    } else if (p.threads == 512) {
+        switch (p.nl) {
+            case 8: return gemv_run<T, MR, 8, 512>(d, stream, p.nslices);
+        }
+    }
     return TV_E_UNSUPPORTED;
 }
 
 template <typename T>
 static int gemv_dispatch_mr(const GemmDesc& d, hipStream_t stream, const GemvPlan& p) {
-    if (d.M <= 1) return gemv_dispatch_cfg<T, 1>(d, stream, p);
-    if (d.M <= 2) return gemv_dispatch_cfg<T, 2>(d, stream, p);
-    if (d.M <= 4) return gemv_dispatch_cfg<T, 4>(d, stream, p);
-    return gemv_dispatch_cfg<T, 8>(d, stream, p);
+    if (d.M <= 1) return gemv_dispatch_nl<T, 1>(d, stream, p);
+    if (d.M <= 2) return gemv_dispatch_nl<T, 2>(d, stream, p);
+    if (d.M <= 4) return gemv_dispatch_nl<T, 4>(d, stream, p);
+    return gemv_dispatch_nl<T, 8>(d, stream, p);
 }
 
 int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices) {

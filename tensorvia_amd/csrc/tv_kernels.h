@@ -46,6 +46,23 @@ int launch_gemv(const GemmDesc& d, hipStream_t stream); // TV_E_UNSUPPORTED if i
 // GEMV with an explicit strip width (nl lanes), workgroup size and K split (tuning sweeps).
 int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices);
 
+// Buffer loads: a lane offset at or above 2^31 is outside every buffer resource built by make_rsrc
+// (num_records <= 2^30), also after a stride multiple below 2^30 is added to it, and such a load
+// returns zeros.
+constexpr unsigned kOOB = 0x80000000u;
+
+__device__ inline u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+// Streaming variant (nontemporal: the lines are not kept in the caches for reuse).
+__device__ inline u32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2));
+}
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const char* base, int64_t bytes) {
+    const int nr = bytes <= 0 ? 0 : (bytes > 0x40000000 ? 0x40000000 : (int)bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, nr, 0x00020000);
+}
+
 __host__ __device__ inline size_t dtype_size(int dt) {
     switch (dt) {
         case TV_INT8: return 1;
