@@ -53,7 +53,7 @@ def _stale(target: Path, deps: list[Path]) -> bool:
 def build_kernels(verbose: bool = False, force: bool = True) -> Path:
     """Compile libtv_hip.so (the extern "C" kernel library) for ``ARCH``."""
     BUILD.mkdir(exist_ok=True)
-    headers = [INCLUDE / "tensorvia_hip.h", CSRC / "tv_kernels.h", CSRC / "gemm_mfma_impl.h"]
+    headers = [INCLUDE / "tensorvia_hip.h", CSRC / "tv_kernels.h", CSRC / "gemm_mfma_impl.h", CSRC / "gemm_dma_impl.h"]
     jobs = []
     objs = []
     for src in KERNEL_SOURCES:

@@ -1,0 +1,353 @@
+// MFMA GEMM with global -> LDS direct loads (gfx950 buffer_load_dwordx4 ... lds) for the 16-bit and
+// int8 inputs when both operands have a vector layout (K- or M/N-contiguous).  Same tile math as
+// gemm_mfma_kernel (gemm_mfma_impl.h); what changes is how a k-tile reaches LDS and the pipeline:
+//
+//  * Loads go straight from HBM/L2 into LDS: no staging registers, no ds_write, no wait for the
+//    loaded data in the wave that issued it.  Each wave instruction fills one contiguous 1 KB block
+//    of LDS (lane l writes bytes 16l..16l+15 of the block), so the layouts are chosen so that every
+//    1 KB block is a set of whole rows and the swizzle is applied by choosing which global chunk each
+//    lane loads:
+//      K-contiguous operand   -> rows of 128 bytes of k, chunk c of row r at c ^ ((r >> 1) & 7)
+//                                (as gemm_mfma_kernel); a block is 8 rows;
+//      M/N-contiguous operand -> k rows of ROWS elements (256 or 512 bytes, no padding), 16-byte
+//                                chunk q of k row r at q ^ swz(r); a block is 4 (int8) or 2 (16-bit)
+//                                k rows.  swz spreads the k rows that one ds_read_b64_tr_b8/_b16
+//                                pass reads over all 64 banks.
+//    Lanes past the matrix edge (rows, columns or k) get an out-of-range buffer offset; the load then
+//    writes zeros into LDS.
+//  * Two LDS stages, S0 and S1, are separate arrays and the k-loop is unrolled by two, so each LDS
+//    read names the stage it reads and the compiler waits only for loads into that stage.
+//  * B fragments are double-buffered in registers; each A fragment block is reloaded with the next
+//    k-group's right after its last MFMA.  One barrier per k-tile:
+//        read B of k-group 1 (tile t); MFMAs of k-group 0, reloading A blocks for k-group 1;
+//        MFMAs of k-group 1 on the first half of the A blocks;
+//        wait for tile t+1's loads; barrier (tile t+1 visible everywhere, stage of tile t free);
+//        load tile t+2 into the stage of tile t; read B and the first A blocks of tile t+1;
+//        MFMAs on the other half, reloading those A blocks for tile t+1.
+#pragma once
+#include "gemm_mfma_impl.h"
+
+namespace tvk {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt on vector-memory operations only (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt
+// and lgkmcnt at their maxima, i.e. not waited for).
+template <int N> __device__ inline void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int MODE, int ROWS, int THREADS, int ES>
+struct DmaOperand {
+    static constexpr int VEC = 16 / ES;            // elements per 16-byte chunk
+    static constexpr int BK = 128 / ES;            // k extent of one k-tile
+    static constexpr int BYTES = ROWS * 128;       // LDS bytes of one k-tile
+    static constexpr int NWAVES = THREADS / 64;
+    static constexpr int NBLK = BYTES / 1024;      // 1 KB load blocks per k-tile
+    static constexpr int PER_WAVE = NBLK / NWAVES; // load instructions per wave per k-tile
+    static constexpr int RB = ROWS * ES;           // M/N layout: bytes per k row
+    static constexpr int CPR = RB / 16;            // M/N layout: chunks per k row
+    static constexpr int KRB = 1024 / RB;          // M/N layout: k rows per block
+    static_assert(NBLK % NWAVES == 0, "load blocks must divide over the waves");
+    static_assert(MODE == LOAD_KCONTIG || (MODE == LOAD_MNCONTIG && ES <= 2 && RB == 256 * ES && ROWS == 256),
+                  "M/N layout is laid out for 256-row int8 / 16-bit tiles");
+
+    const char* base; // element (row0, k = 0) of this tile, as bytes
+    int64_t s_r, s_k; // element strides
+    int rows_valid;   // rows of this tile inside the matrix
+    int K;
+    unsigned loff[PER_WAVE]; // lane byte offsets from the k-tile origin (kOOB past the matrix rows)
+    int kc[PER_WAVE];        // K layout: first k of the lane's chunk inside the k-tile
+
+    // M/N layout swizzle: distinct 16-byte bank groups for the k rows one transpose-read pass reads.
+    __device__ static inline int swz(int kr) {
+        if constexpr (ES == 1) return (kr & 7) | (((kr >> 4) & 1) << 3);
+        else return ((kr & 3) | (((kr >> 3) & 1) << 2)) << 1;
+    }
+
+    __device__ inline void init(int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) {
+            const int blk = wave * PER_WAVE + j;
+            if constexpr (MODE == LOAD_KCONTIG) {
+                const int row = blk * 8 + (lane >> 3);
+                const int c = (lane & 7) ^ ((row >> 1) & 7);
+                loff[j] = row < rows_valid ? (unsigned)((int64_t)row * s_r * ES + c * 16) : kOOB;
+                kc[j] = c * VEC;
+            } else {
+                const int kr = blk * KRB + lane / CPR;
+                const int q = (lane % CPR) ^ swz(kr);
+                loff[j] = q * VEC < rows_valid ? (unsigned)((int64_t)kr * s_k * ES + q * 16) : kOOB;
+                kc[j] = 0;
+            }
+        }
+    }
+
+    // Loads k-tile k0 into `stage` (this wave's PER_WAVE blocks).
+    __device__ inline void issue(char* stage, int wave, int k0) const {
+        __amdgpu_buffer_rsrc_t rs;
+        if constexpr (MODE == LOAD_KCONTIG) {
+            const int rows = rows_valid < ROWS ? rows_valid : ROWS;
+            rs = make_rsrc(base + (int64_t)k0 * ES, (int64_t)rows * s_r * ES);
+        } else {
+            rs = make_rsrc(base + (int64_t)k0 * s_k * ES, (int64_t)(K - k0) * s_k * ES);
+        }
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) {
+            unsigned off = loff[j];
+            if constexpr (MODE == LOAD_KCONTIG) off = k0 + kc[j] < K ? off : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(stage + (wave * PER_WAVE + j) * 1024), 16, off, 0, 0, 0);
+        }
+    }
+
+    // Fragment addressing (see TileLoader::frag for the lane -> k assignment).
+    //  K layout: b128 at kc_off(w0 + 16f + lane%16, 4kg + lane/16).
+    //  M/N layout, int8:  lanes 2r+c of group g read k row 64kg + 16g + r (+8 for the second read),
+    //                     bytes 8c..8c+7 of chunk w0/16 + f;
+    //  M/N layout, 16-bit: lanes 4r+c of group g read k row 32kg + 8g + r (+4), bytes 8c..8c+7 of the
+    //                     32-byte pair of chunks starting at w0/8 + 2f.
+    int fb_lo[2], fb_hi[2]; // byte offset of the lane's k row (+ in-chunk offset), first / second read
+    int sw_lo[2], sw_hi[2]; // swizzle of those k rows
+    int q0;                 // first chunk of the wave's rows (M/N layout)
+    int fbase[2];           // K layout
+
+    __device__ inline void frag_init(int lane, int w0) {
+        const int fr = lane & 15, grp = lane >> 4;
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg) {
+            if constexpr (MODE == LOAD_KCONTIG) {
+                fbase[kg] = kc_off(w0 + fr, kg * 4 + grp);
+            } else if constexpr (ES == 1) {
+                const int kr = kg * 64 + grp * 16 + (fr >> 1);
+                fb_lo[kg] = kr * RB + (fr & 1) * 8;
+                fb_hi[kg] = (kr + 8) * RB + (fr & 1) * 8;
+                sw_lo[kg] = swz(kr);
+                sw_hi[kg] = swz(kr + 8);
+            } else {
+                const int kr = kg * 32 + grp * 8 + (fr >> 2);
+                const int c = fr & 3;
+                fb_lo[kg] = kr * RB + (c >> 1) * 16 + (c & 1) * 8;
+                fb_hi[kg] = (kr + 4) * RB + (c >> 1) * 16 + (c & 1) * 8;
+                sw_lo[kg] = swz(kr);
+                sw_hi[kg] = swz(kr + 4);
+            }
+        }
+        q0 = ES == 1 ? w0 / 16 : w0 / 8;
+    }
+
+    __device__ inline u32x4 frag(const char* stage, int kg, int f) const {
+        if constexpr (MODE == LOAD_KCONTIG) {
+            return *reinterpret_cast<const u32x4*>(stage + fbase[kg] + f * 2048);
+        } else if constexpr (ES == 1) {
+            const int q = q0 + f;
+            const lds_char* lo = (const lds_char*)(stage + fb_lo[kg] + ((q ^ sw_lo[kg]) << 4));
+            const lds_char* hi = (const lds_char*)(stage + fb_hi[kg] + ((q ^ sw_hi[kg]) << 4));
+            const i32x2_t a = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)lo);
+            const i32x2_t b = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)hi);
+            return u32x4{(unsigned)a.x, (unsigned)a.y, (unsigned)b.x, (unsigned)b.y};
+        } else {
+            const int q = q0 + 2 * f;
+            const lds_char* lo = (const lds_char*)(stage + fb_lo[kg] + ((q ^ sw_lo[kg]) << 4));
+            const lds_char* hi = (const lds_char*)(stage + fb_hi[kg] + ((q ^ sw_hi[kg]) << 4));
+            const i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)lo);
+            const i16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)hi);
+            const uint2 l2 = __builtin_bit_cast(uint2, a), h2 = __builtin_bit_cast(uint2, b);
+            return u32x4{l2.x, l2.y, h2.x, h2.y};
+        }
+    }
+
+    static constexpr int kFragReads = MODE == LOAD_MNCONTIG ? 2 : 1;
+};
+
+template <class C>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
+                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
+void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec) {
+    using T = typename C::T;
+    using Op = Mfma<T>;
+    using Acc = typename Op::Acc;
+    constexpr int ES = C::ES;
+    using LA = DmaOperand<C::AMODE, C::BM, C::THREADS, ES>;
+    using LB = DmaOperand<C::BMODE, C::BN, C::THREADS, ES>;
+    constexpr int STAGE = LA::BYTES + LB::BYTES;
+    constexpr int NWAVES = C::THREADS / 64;
+    static_assert(NWAVES % 2 == 0, "the epilogue gives half of the waves to each stage array");
+    constexpr int EPI = STAGE / (NWAVES / 2) / 16 * 16; // staging bytes per wave in the epilogue
+
+    __shared__ __attribute__((aligned(1024))) char S0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char S1[STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+
+    // Workgroup -> tile (XCD-aware, groups of group_m tile-rows), as gemm_mfma_kernel.
+    int bid = blockIdx.x;
+    const int nwg = gridDim.x;
+    if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+    const int per_batch = tiles_m * tiles_n;
+    const int b = bid / per_batch;
+    int r = bid - b * per_batch;
+    const int span = group_m * tiles_n;
+    const int g = r / span;
+    const int first_m = g * group_m;
+    const int gsz = min(tiles_m - first_m, group_m);
+    r -= g * span;
+    const int tm = first_m + r % gsz;
+    const int tn = r / gsz;
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
+
+    LA la;
+    la.base = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + (int64_t)m0 * d.sa_m) * ES;
+    la.s_r = d.sa_m; la.s_k = d.sa_k; la.rows_valid = d.M - m0; la.K = d.K;
+    LB lb;
+    lb.base = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)n0 * d.sb_n) * ES;
+    lb.s_r = d.sb_n; lb.s_k = d.sb_k; lb.rows_valid = d.N - n0; lb.K = d.K;
+    la.init(wave, lane);
+    lb.init(wave, lane);
+    la.frag_init(lane, wm * C::WM);
+    lb.frag_init(lane, wn * C::WN);
+
+    Acc acc[C::FM][C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+
+    // A fragments: one set, each block reloaded with the next k-group's right after its last MFMA.
+    // B fragments: double-buffered (every A block of a k-group uses all of them).
+    u32x4 fa[C::FM], fb0[C::FN], fb1[C::FN];
+    auto read_b = [&](const char* stage, int kg, u32x4 (&fb)[C::FN]) {
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) fb[j] = lb.frag(stage + LA::BYTES, kg, j);
+    };
+    auto row = [&](int i, const u32x4 (&fb)[C::FN]) {
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) Op::run(fb[j], fa[i], acc[i][j]); // B fragment first: lanes hold 4 columns
+    };
+    auto load_tile = [&](char* stage, int kt) {
+        la.issue(stage, wave, kt * C::BK);
+        lb.issue(stage + LA::BYTES, wave, kt * C::BK);
+    };
+    constexpr int H = C::FM / 2;
+
+    // One k-tile in stage `sc`; tile kt+1 is being loaded into `sn`.  On entry fa / fb0 hold k-group
+    // 0 of tile kt.
+    auto step = [&](char* sc, char* sn, int kt, int nk) {
+        read_b(sc, 1, fb1);
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i) {
+            row(i, fb0);
+            fa[i] = la.frag(sc, 1, i);
+        }
+#pragma unroll
+        for (int i = 0; i < H; ++i) row(i, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        // Tile kt+1 (the only loads in flight) has landed in this wave's blocks; after the barrier
+        // it has landed everywhere and every wave is done reading `sc`.
+        wait_vmcnt<0>();
+        lds_barrier();
+        // Unconditional: past the last tile every lane is out of range and the loads write zeros
+        // into `sc`, which is not read again.  (A branch here would also make the compiler wait for
+        // all loads before any LDS read after the join.)
+        load_tile(sc, kt + 2);
+        read_b(sn, 0, fb0);
+#pragma unroll
+        for (int i = 0; i < H; ++i) fa[i] = la.frag(sn, 0, i);
+#pragma unroll
+        for (int i = H; i < C::FM; ++i) {
+            row(i, fb1);
+            fa[i] = la.frag(sn, 0, i);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const int nk = (d.K + C::BK - 1) / C::BK;
+    // Prologue: tiles 0 and 1 in flight, then F0 of tile 0.
+    load_tile(S0, 0);
+    load_tile(S1, 1); // all out of range (zeros) when nk == 1
+    constexpr int NDMA = LA::PER_WAVE + LB::PER_WAVE; // loads per k-tile and wave
+    wait_vmcnt<NDMA>();
+    lds_barrier();
+    read_b(S0, 0, fb0);
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) fa[i] = la.frag(S0, 0, i);
+
+    // The step count is rounded up to even: a step past K multiplies the zeros loaded there, and
+    // the loop has no conditional tail (the accumulators stay in place across the loop).
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(S0, S1, kt, nk);
+        step(S1, S0, kt + 1, nk);
+    }
+
+    // Epilogue.  The zero-filling loads issued by the last steps land before anything else (no
+    // load into LDS is left in flight when the workgroup ends); all waves leave the k-loop's LDS
+    // before any wave stages its output there.
+    wait_vmcnt<0>();
+    const size_t csz = dtype_size(d.dtype_c);
+    char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
+    if (c_vec == 2) {
+        lds_barrier();
+        char* lw = (wave < NWAVES / 2 ? S0 : S1) + (wave % (NWAVES / 2)) * EPI;
+        const int mrow0 = m0 + wm * C::WM, ncol0 = n0 + wn * C::WN;
+        if constexpr (__is_same(Acc, i32x4)) {
+            if (d.dtype_c == TV_INT8) write_tile_staged<int8_t, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d);
+            else write_tile_staged<int32_t, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d);
+        } else {
+            if (d.dtype_c == TV_BFLOAT16) write_tile_staged<__bf16, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d);
+            else if (d.dtype_c == TV_FLOAT16) write_tile_staged<_Float16, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d);
+            else write_tile_staged<float, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d);
+        }
+        return;
+    }
+    const int row0 = m0 + wm * C::WM + (lane & 15);
+    const int col0 = n0 + wn * C::WN + (lane >> 4) * 4;
+    const bool vec_ok = c_vec != 0;
+    if constexpr (__is_same(Acc, i32x4)) {
+        if (d.dtype_c == TV_INT8) write_tile<int8_t, C>(acc, Cb, row0, col0, vec_ok, d);
+        else write_tile<int32_t, C>(acc, Cb, row0, col0, vec_ok, d);
+    } else {
+        if (d.dtype_c == TV_BFLOAT16) write_tile<__bf16, C>(acc, Cb, row0, col0, vec_ok, d);
+        else if (d.dtype_c == TV_FLOAT16) write_tile<_Float16, C>(acc, Cb, row0, col0, vec_ok, d);
+        else write_tile<float, C>(acc, Cb, row0, col0, vec_ok, d);
+    }
+}
+
+template <class C>
+static int run_dma_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
+    const int tiles_m = (d.M + C::BM - 1) / C::BM;
+    const int tiles_n = (d.N + C::BN - 1) / C::BN;
+    const int64_t nwg = (int64_t)tiles_m * tiles_n * d.batch;
+    if (nwg <= 0) return 0;
+    if (nwg > 0x7FFFFFFF) return TV_E_SHAPE;
+    const size_t csz = dtype_size(d.dtype_c);
+    int c_vec = d.sc_n == 1 && d.sc_m % 4 == 0 && (d.batch <= 1 || d.sc_b % 4 == 0) &&
+                (reinterpret_cast<uintptr_t>(d.C) % (4 * csz)) == 0;
+    const int64_t v16 = 16 / (int64_t)csz;
+    if (c_vec && d.sc_m % v16 == 0 && (d.batch <= 1 || d.sc_b % v16 == 0) &&
+        (reinterpret_cast<uintptr_t>(d.C) % 16) == 0 && (C::WN * (int64_t)csz) % 16 == 0)
+        c_vec = 2;
+    hipLaunchKernelGGL(gemm_dma_kernel<C>, dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
+                       group_m, c_vec);
+    return hipGetLastError();
+}
+
+// 16-bit / int8 inputs: direct-to-LDS kernel for the vector layouts, gemm_mfma_kernel otherwise.
+template <typename T, int BM, int BN, int WMW, int WNW>
+static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m) {
+    const int es = (int)sizeof(T);
+    const int am = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, BM);
+    const int bm = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, BN);
+#define TV_CASE(A_, B_) \
+    if (am == A_ && bm == B_) return run_dma_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream, group_m);
+    TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)
+    TV_CASE(LOAD_KCONTIG, LOAD_KCONTIG)
+    TV_CASE(LOAD_MNCONTIG, LOAD_MNCONTIG)
+    TV_CASE(LOAD_MNCONTIG, LOAD_KCONTIG)
+#undef TV_CASE
+    return run_modes<T, BM, BN, WMW, WNW>(d, stream, group_m);
+}
+
+} // namespace tvk

@@ -1,8 +1,8 @@
 // __bf16 instantiation of the MFMA GEMM kernels (gemm_mfma_impl.h).
-#include "gemm_mfma_impl.h"
+#include "gemm_dma_impl.h"
 
 namespace tvk {
 int launch_gemm_mfma_bf16(const GemmDesc& d, hipStream_t stream) {
-    return run_modes<__bf16, 256, 256, 2, 4>(d, stream, 8);
+    return run_modes_dma<__bf16, 256, 256, 2, 4>(d, stream, 8);
 }
 } // namespace tvk

@@ -1,8 +1,8 @@
 // _Float16 instantiation of the MFMA GEMM kernels (gemm_mfma_impl.h).
-#include "gemm_mfma_impl.h"
+#include "gemm_dma_impl.h"
 
 namespace tvk {
 int launch_gemm_mfma_f16(const GemmDesc& d, hipStream_t stream) {
-    return run_modes<_Float16, 256, 256, 2, 4>(d, stream, 8);
+    return run_modes_dma<_Float16, 256, 256, 2, 4>(d, stream, 8);
 }
 } // namespace tvk

@@ -1,8 +1,8 @@
 // int8_t instantiation of the MFMA GEMM kernels (gemm_mfma_impl.h).
-#include "gemm_mfma_impl.h"
+#include "gemm_dma_impl.h"
 
 namespace tvk {
 int launch_gemm_mfma_i8(const GemmDesc& d, hipStream_t stream) {
-    return run_modes<int8_t, 256, 256, 2, 4>(d, stream, 8);
+    return run_modes_dma<int8_t, 256, 256, 2, 4>(d, stream, 8);
 }
 } // namespace tvk

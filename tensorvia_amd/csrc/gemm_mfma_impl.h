@@ -315,15 +315,22 @@ constexpr int kEpiWaveBytes = 18432;
 // in 16-byte row chunks, so every global store covers whole row segments.  Rows are processed in
 // passes of RPP (all WM rows for 1- and 2-byte outputs).  Requires a contiguous row (sc_n == 1)
 // with 16-byte aligned row starts at the tile's column origin.
-template <typename TC, class C, typename Acc>
+// Rows per staging pass: the largest of WM, WM/2, WM/4, ... (a multiple of 16) whose padded rows
+// fit in the wave's staging bytes.
+template <int WM, int PITCH, int WAVE_BYTES> constexpr int staged_rows() {
+    int r = WM;
+    while (r > 16 && r * PITCH > WAVE_BYTES) r /= 2;
+    return r;
+}
+
+template <typename TC, class C, typename Acc, int WAVE_BYTES = kEpiWaveBytes>
 __device__ inline void write_tile_staged(const Acc (&acc)[C::FM][C::FN], char* lds_wave, char* Cb, int lane, int mrow0,
                                          int ncol0, const GemmDesc& d) {
     constexpr int ROWB = C::WN * (int)sizeof(TC);            // bytes per output row of the wave tile
     constexpr int PITCH = ROWB + 16;
-    constexpr int RPP0 = kEpiWaveBytes / PITCH / 16 * 16;
-    constexpr int RPP = RPP0 < C::WM ? RPP0 : C::WM;          // rows per pass
+    constexpr int RPP = staged_rows<C::WM, PITCH, WAVE_BYTES>(); // rows per pass
     constexpr int CPR = ROWB / 16;                            // 16-byte chunks per row
-    static_assert(RPP >= 16 && C::WM % RPP == 0, "staging area too small");
+    static_assert(RPP >= 16 && C::WM % RPP == 0 && RPP * PITCH <= WAVE_BYTES, "staging area too small");
     typedef TC vec_t __attribute__((__vector_size__(4 * sizeof(TC))));
 #pragma unroll
     for (int pass = 0; pass < C::WM / RPP; ++pass) {
