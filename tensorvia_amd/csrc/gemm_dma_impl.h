@@ -38,6 +38,24 @@ template <int N> __device__ inline void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Workgroup barrier for the direct-load pipeline: this wave's LDS reads have completed (lgkmcnt)
+// and no memory access moves across it.  Loads into LDS are waited for explicitly (vmcnt), so
+// other memory operations stay in flight (a release fence on LDS would wait for all of them).
+__device__ inline void dma_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The same direct load, hidden from the compiler: it then adds no waits of its own for the LDS it
+// writes (callers wait with explicit vmcnt counts).  M0 is written right before the load; the
+// s_nop covers the M0 and descriptor-register read-after-write wait states.
+__device__ inline void dma_load16_asm(__amdgpu_buffer_rsrc_t r, char* lds_dst, unsigned off) {
+    const unsigned m0v = (unsigned)(uintptr_t)(lds_void*)lds_dst;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(off), "s"(r)
+                 : "memory", "m0");
+}
+
 template <int MODE, int ROWS, int THREADS, int ES>
 struct DmaOperand {
     static constexpr int VEC = 16 / ES;            // elements per 16-byte chunk
@@ -84,7 +102,8 @@ struct DmaOperand {
         }
     }
 
-    // Loads k-tile k0 into `stage` (this wave's PER_WAVE blocks).
+    // Loads k-tile k0 into `stage` (this wave's PER_WAVE blocks); ASM: through dma_load16_asm.
+    template <bool ASM = false>
     __device__ inline void issue(char* stage, int wave, int k0) const {
         __amdgpu_buffer_rsrc_t rs;
         if constexpr (MODE == LOAD_KCONTIG) {
@@ -97,7 +116,10 @@ struct DmaOperand {
         for (int j = 0; j < PER_WAVE; ++j) {
             unsigned off = loff[j];
             if constexpr (MODE == LOAD_KCONTIG) off = k0 + kc[j] < K ? off : kOOB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(stage + (wave * PER_WAVE + j) * 1024), 16, off, 0, 0, 0);
+            if constexpr (ASM)
+                dma_load16_asm(rs, stage + (wave * PER_WAVE + j) * 1024, off);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(stage + (wave * PER_WAVE + j) * 1024), 16, off, 0, 0, 0);
         }
     }
 
@@ -315,6 +337,181 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Small K (at most two 128-byte k-tiles, e.g. attention scores Q @ K^T with head dim 128): the
+// output dominates, and a workgroup per tile would load, compute and store one after the other.
+// Persistent workgroups (one per CU) take contiguous runs of tiles; A stays in LDS while the run
+// stays in one block of rows, and B of the next tile loads while the current tile's output leaves
+// through a separate staging area.
+constexpr int kSmallKEpiBytes = 2304; // per wave: 16 rows of a 64-column 16-bit or 8-bit output row
+
+// Staged store for the small-K kernel: as write_tile_staged, but every wave issues the same number
+// of 16-byte buffer stores (chunks outside the matrix get an out-of-range offset and are dropped),
+// so a later vmcnt wait can count them.  Requires N and the row pitch in whole 16-byte chunks.
+// The stores are nontemporal (nt): the output is written once and never re-read by this launch,
+// and streaming it past the caches keeps them for the next tile's B and the resident A
+// (c4 fp16: 99.7 -> 73.1 us).
+template <typename TC, class C, typename Acc, int WAVE_BYTES>
+__device__ inline void write_tile_fixed(const Acc (&acc)[C::FM][C::FN], char* lds_wave, __amdgpu_buffer_rsrc_t cr,
+                                        int lane, int mrow0, int ncol0, const GemmDesc& d) {
+    constexpr int ROWB = C::WN * (int)sizeof(TC);
+    constexpr int PITCH = ROWB + 16;
+    constexpr int RPP = staged_rows<C::WM, PITCH, WAVE_BYTES>();
+    constexpr int CPR = ROWB / 16;
+    static_assert(RPP >= 16 && C::WM % RPP == 0 && RPP * PITCH <= WAVE_BYTES && (RPP * CPR) % 64 == 0,
+                  "staging pass must be whole wave stores");
+    typedef TC vec_t __attribute__((__vector_size__(4 * sizeof(TC))));
+#pragma unroll
+    for (int pass = 0; pass < C::WM / RPP; ++pass) {
+#pragma unroll
+        for (int i = pass * (RPP / 16); i < (pass + 1) * (RPP / 16); ++i) {
+            char* rowp = lds_wave + (16 * (i - pass * (RPP / 16)) + (lane & 15)) * PITCH + (lane >> 4) * 4 * sizeof(TC);
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) {
+                vec_t v;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = cvt_out<TC>(acc[i][j][q]);
+                *reinterpret_cast<vec_t*>(rowp + j * 16 * sizeof(TC)) = v;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+        for (int u = 0; u < RPP * CPR / 64; ++u) {
+            const int idx = lane + 64 * u;
+            const int r = idx / CPR, c = idx % CPR;
+            const int row = mrow0 + pass * RPP + r;
+            const int col = ncol0 + c * (16 / (int)sizeof(TC));
+            const u32x4 v = *reinterpret_cast<const u32x4*>(lds_wave + r * PITCH + c * 16);
+            const unsigned off = row < d.M && col < d.N ? (unsigned)(((int64_t)row * d.sc_m + col) * (int64_t)sizeof(TC)) : kOOB;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), cr, (int)off, 0, 2);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    }
+}
+
+template <class C>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
+                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
+void gemm_smallk_kernel(GemmDesc d, int tiles_m, int tiles_n) {
+    using T = typename C::T;
+    using Op = Mfma<T>;
+    using Acc = typename Op::Acc;
+    constexpr int ES = C::ES;
+    using LA = DmaOperand<C::AMODE, C::BM, C::THREADS, ES>;
+    using LB = DmaOperand<C::BMODE, C::BN, C::THREADS, ES>;
+    constexpr int NWAVES = C::THREADS / 64;
+    constexpr int EPI = kSmallKEpiBytes;
+
+    // A's two k-tiles stay resident while consecutive tiles share them (same batch and rows); B's
+    // two k-tiles are reloaded per tile.
+    __shared__ __attribute__((aligned(1024))) char SA[2 * LA::BYTES];
+    __shared__ __attribute__((aligned(1024))) char SB[2 * LB::BYTES];
+    __shared__ __attribute__((aligned(16))) char E[EPI * NWAVES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+    const int per_batch = tiles_m * tiles_n;
+    const int ntiles = per_batch * d.batch;
+
+    LA la;
+    LB lb;
+    la.s_r = d.sa_m; la.s_k = d.sa_k; la.K = d.K;
+    lb.s_r = d.sb_n; lb.s_k = d.sb_k; lb.K = d.K;
+    la.frag_init(lane, wm * C::WM);
+    lb.frag_init(lane, wn * C::WN);
+
+    // Workgroup w takes the contiguous tiles [w*ntiles/G, (w+1)*ntiles/G) in (batch, m, n) order, so
+    // consecutive tiles share A; ids are remapped so that neighbouring ranges (same batch, sharing
+    // B) run on one XCD.
+    const int G = gridDim.x;
+    int w = blockIdx.x;
+    if ((G & 7) == 0) w = (w & 7) * (G >> 3) + (w >> 3);
+    const int t_end = (int)((int64_t)(w + 1) * ntiles / G);
+
+    // Points the loaders at tile t and loads its k-tiles (A only when it changes).  Past t_end every
+    // lane is out of range and nothing is read.
+    int cur_b = -1, cur_m0 = -1;
+    auto start = [&](int t, int& b, int& m0, int& n0) {
+        const bool live = t < t_end;
+        const int tt = live ? t : t_end - 1;
+        b = tt / per_batch;
+        const int r = tt - b * per_batch;
+        m0 = (r / tiles_n) * C::BM;
+        n0 = (r % tiles_n) * C::BN;
+        lb.base = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)n0 * d.sb_n) * ES;
+        lb.rows_valid = live ? d.N - n0 : 0;
+        lb.init(wave, lane);
+        lb.template issue<true>(SB, wave, 0);
+        lb.template issue<true>(SB + LB::BYTES, wave, C::BK); // zeros when K fits in one k-tile
+        if (live && (b != cur_b || m0 != cur_m0)) { // uniform over the workgroup
+            cur_b = b;
+            cur_m0 = m0;
+            la.base = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + (int64_t)m0 * d.sa_m) * ES;
+            la.rows_valid = d.M - m0;
+            la.init(wave, lane);
+            la.template issue<true>(SA, wave, 0);
+            la.template issue<true>(SA + LA::BYTES, wave, C::BK);
+        }
+    };
+
+    int t = (int)((int64_t)w * ntiles / G), b, m0, n0;
+    start(t, b, m0, n0);
+    const size_t csz = dtype_size(d.dtype_c);
+    constexpr int NST = C::WM * (C::WN * ES / 16) / 64; // epilogue stores per wave (output type = input size)
+    wait_vmcnt<0>();
+    for (;;) {
+        dma_barrier(); // this tile's operands have landed everywhere
+        Acc acc[C::FM][C::FN];
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+        // Both k-tiles, always (the second holds zeros when K fits in one).
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int kg = 0; kg < 2; ++kg) {
+                u32x4 fa[C::FM], fb[C::FN];
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j) fb[j] = lb.frag(SB + kt * LB::BYTES, kg, j);
+#pragma unroll
+                for (int i = 0; i < C::FM; ++i) fa[i] = la.frag(SA + kt * LA::BYTES, kg, i);
+#pragma unroll
+                for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < C::FN; ++j) Op::run(fb[j], fa[i], acc[i][j]);
+            }
+        }
+        dma_barrier(); // every wave is done reading the operands
+        const int cb = b, cm0 = m0, cn0 = n0;
+        const int next = t + 1;
+        start(next, b, m0, n0);
+        // The output of tile t leaves while the next tile's operands load.
+        const char* Cb = static_cast<const char*>(d.C) + (int64_t)cb * d.sc_b * csz;
+        const __amdgpu_buffer_rsrc_t cr = make_rsrc(Cb, ((int64_t)(d.M - 1) * d.sc_m + d.N) * (int64_t)csz);
+        char* lw = E + wave * EPI;
+        const int mrow0 = cm0 + wm * C::WM, ncol0 = cn0 + wn * C::WN;
+        if constexpr (__is_same(Acc, i32x4)) {
+            write_tile_fixed<int8_t, C, Acc, EPI>(acc, lw, cr, lane, mrow0, ncol0, d);
+        } else {
+            if (d.dtype_c == TV_BFLOAT16) write_tile_fixed<__bf16, C, Acc, EPI>(acc, lw, cr, lane, mrow0, ncol0, d);
+            else write_tile_fixed<_Float16, C, Acc, EPI>(acc, lw, cr, lane, mrow0, ncol0, d);
+        }
+        if (next >= t_end) break;
+        t = next;
+        // The next tile's operands were loaded before this tile's NST stores (vmcnt retires in issue
+        // order), so waiting down to NST outstanding operations leaves only the stores in flight.
+        wait_vmcnt<NST>();
+    }
+    wait_vmcnt<0>();
+}
+
 template <class C>
 static int run_dma_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
     const int tiles_m = (d.M + C::BM - 1) / C::BM;
@@ -334,12 +531,49 @@ static int run_dma_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
     return hipGetLastError();
 }
 
+// Small-K path: K within two 128-byte k-tiles, an 8- or 16-bit output (int8 inputs: int8 output;
+// half inputs: half output) with 16-byte aligned rows, and enough tiles to keep every CU busy.
+template <class C>
+static int run_smallk_cfg(const GemmDesc& d, hipStream_t stream) {
+    const int tiles_m = (d.M + C::BM - 1) / C::BM;
+    const int tiles_n = (d.N + C::BN - 1) / C::BN;
+    const int64_t nt = (int64_t)tiles_m * tiles_n * d.batch;
+    if (nt > 0x7FFFFFFF) return TV_E_SHAPE;
+    int cus = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    const int grid = (int)(nt < cus ? nt : cus);
+    hipLaunchKernelGGL(gemm_smallk_kernel<C>, dim3((unsigned)grid), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n);
+    return hipGetLastError();
+}
+
+static bool smallk_ok(const GemmDesc& d, int es, int bm_rows, int bn_rows) {
+    const size_t csz = dtype_size(d.dtype_c);
+    if (d.K > 2 * (128 / es) || csz != (size_t)es) return false;
+    if (d.N % (16 / (int64_t)csz) != 0) return false;
+    if (((int64_t)(d.M - 1) * d.sc_m + d.N) * (int64_t)csz >= ((int64_t)1 << 30)) return false;
+    if (!(d.sc_n == 1 && (reinterpret_cast<uintptr_t>(d.C) % 16) == 0 && d.sc_m % (16 / (int64_t)csz) == 0 &&
+          (d.batch <= 1 || d.sc_b % (16 / (int64_t)csz) == 0)))
+        return false;
+    const int64_t tiles = (int64_t)((d.M + bm_rows - 1) / bm_rows) * ((d.N + bn_rows - 1) / bn_rows) * d.batch;
+    return tiles >= 1024;
+}
+
 // 16-bit / int8 inputs: direct-to-LDS kernel for the vector layouts, gemm_mfma_kernel otherwise.
 template <typename T, int BM, int BN, int WMW, int WNW>
 static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m) {
     const int es = (int)sizeof(T);
     const int am = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, BM);
     const int bm = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, BN);
+    if (am != LOAD_GENERIC && bm != LOAD_GENERIC && smallk_ok(d, es, BM, BN)) {
+#define TV_CASE(A_, B_) \
+    if (am == A_ && bm == B_) return run_smallk_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream);
+        TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)
+        TV_CASE(LOAD_KCONTIG, LOAD_KCONTIG)
+        TV_CASE(LOAD_MNCONTIG, LOAD_MNCONTIG)
+        TV_CASE(LOAD_MNCONTIG, LOAD_KCONTIG)
+#undef TV_CASE
+    }
 #define TV_CASE(A_, B_) \
     if (am == A_ && bm == B_) return run_dma_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream, group_m);
     TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)

@@ -171,9 +171,10 @@ def test_bf16_config3_broadcast_equals_flattened(hip):
 
 
 def test_fp16_config4_transposed_view(hip):
-    """c4 at reduced batch: Q[4,2048,128] @ K.permute(0,2,1) consumed through strides, against the
-    oracle on the materialised transpose (ops::Transpose(K,{0,2,1}) on the CPU)."""
-    Bt, S, D = 4, 2048, 128
+    """c4 at full size: Q[32,2048,128] @ K.permute(0,2,1) consumed through strides (the persistent
+    small-K path), against the oracle on the materialised transpose (ops::Transpose(K,{0,2,1}) on
+    the CPU) for every batch."""
+    Bt, S, D = 32, 2048, 128
     q = half_bits(rng.normal_f32(7, Bt * S * D) / np.float32(np.sqrt(D)), FLOAT16).reshape(Bt, S, D)
     k = half_bits(rng.normal_f32(8, Bt * S * D) / np.float32(np.sqrt(D)), FLOAT16).reshape(Bt, S, D)
     tq, tk = to_torch(q, FLOAT16), to_torch(k, FLOAT16)
@@ -186,6 +187,31 @@ def test_fp16_config4_transposed_view(hip):
     assert_half_close(c[0], ref[0], bound, D)
     for bi in range(1, Bt):
         assert_half_close(c[bi], ref[bi], orc.abs_bound(to_f32(q, FLOAT16)[bi], to_f32(kt, FLOAT16)[bi]), D)
+
+
+@pytest.mark.parametrize("dt", [FLOAT16, BFLOAT16, INT8])
+@pytest.mark.parametrize("K", [16, 72, 128, 256])
+@pytest.mark.parametrize("bt", [False, True])
+def test_small_k_persistent_exact(hip, dt, K, bt):
+    """The persistent small-K path (K within two 128-byte k-tiles, >= 1024 output tiles): ragged
+    256x256 tiles (M=264, N=272), B K-contiguous (transposed view) or N-contiguous, integer-valued
+    inputs whose sums every order reproduces: bit-exact against exact fp64 sums."""
+    if dt != INT8 and K > 128:
+        pytest.skip("16-bit inputs take this path for K <= 128")
+    Bt, M, N = 256, 264, 272
+    x = ints(60 + K, (Bt, M, K), -2, 2)
+    y = ints(61 + K, (Bt, K, N), -2, 2)
+    exact = np.matmul(x.astype(np.float64), y.astype(np.float64))
+    if dt == INT8:
+        xs, ys = x.astype(np.int8), y.astype(np.int8)
+        want = orc.low_byte(exact.astype(np.int64))
+    else:
+        xs, ys = half_bits(x, dt), half_bits(y, dt)
+        want = half_bits(exact.astype(np.float32), dt)
+    a = to_torch(xs, dt)
+    b = to_torch(np.ascontiguousarray(np.swapaxes(ys, 1, 2)), dt).permute(0, 2, 1) if bt else to_torch(ys, dt)
+    c = to_storage(hip.gemm(a, b))
+    np.testing.assert_array_equal(c, want)
 
 
 # ---- views, offsets, batches ----------------------------------------------------------------
