@@ -8,6 +8,7 @@ in the same run and reported under ``configs``.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c2,...] [--no-cpu]
                        [--only c2]   (only that config's kernel, e.g. under rocprofv3)
+                       [--vendor]    (also time torch's own library GEMM on the same inputs)
 """
 from __future__ import annotations
 
@@ -149,6 +150,49 @@ def run_gpu(name: str, steps: int, warmup: int):
     return res, inp
 
 
+def run_vendor(name: str, inp, steps: int, warmup: int) -> dict:
+    """The same configuration through torch's own GEMM (hipBLASLt / rocBLAS on ROCm), for comparison.
+
+    Differences from the measured path: c2 uses torch._int_mm (int32 output: the library has no
+    int8-output int8 GEMM); c4 multiplies by a materialised K^T (batched half products on a
+    transposed right operand are avoided on this platform)."""
+    import torch
+
+    from tensorvia_amd.matmul import storage_to_torch as to_torch
+    dt = inp["dt"]
+    a = to_torch(inp["a"], dt)
+    b = to_torch(inp["b"], dt)
+    note = "torch.matmul"
+    if name == "c2":
+        fn = lambda i: torch._int_mm(a, b)
+        note = "torch._int_mm (int32 output)"
+    elif name == "c4":
+        bt = b.permute(0, 2, 1).contiguous()
+        fn = lambda i: torch.bmm(a, bt)
+        note = "torch.bmm with K^T materialised"
+    else:
+        reps = [b] + ([b.clone() for _ in range(5)] if name.startswith("c5") else [])
+        fn = lambda i: torch.matmul(a, reps[i % len(reps)])
+        if name.startswith("c5"):
+            note = "torch.matmul, 6 W replicas rotated"
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(steps):
+        fn(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    flops, bytes_ = work(name, inp)
+    res = {"call": note, "ms_mean": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+           "tflops_frac_peak": flops / (ms * 1e-3) / 1e12 / PEAK[DTYPE[name]], "hbm_gbs": bytes_ / (ms * 1e-3) / 1e9}
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_copy(steps: int, warmup: int) -> dict:
     """Calibration for the HBM traffic counters: a plain device copy of a known size (512 MiB read,
     512 MiB written per launch; larger than the 256 MB MALL)."""
@@ -212,6 +256,7 @@ def main() -> int:
                     help="run only this config's GPU kernel (for profilers); 'copy' runs the traffic calibration copy")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-all", action="store_true", help="CPU baseline for every config, not only c2")
+    ap.add_argument("--vendor", action="store_true", help="also time torch's library GEMM on the same inputs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -238,6 +283,10 @@ def main() -> int:
         results[n], inputs[n] = run_gpu(n, args.steps, args.warmup)
         log(f"gpu {n}: {results[n]['kernel_ms_mean'] * 1e3:.1f} us  {results[n]['tflops']:.1f} T/s  "
             f"{results[n]['hbm_gbs']:.0f} GB/s")
+        if args.vendor:
+            v = run_vendor(n, inputs[n], args.steps, args.warmup)
+            results[n]["torch_library"] = v
+            log(f"torch {n}: {v['ms_mean'] * 1e3:.1f} us  {v['tflops']:.1f} T/s  {v['hbm_gbs']:.0f} GB/s  ({v['call']})")
     if args.only:
         print(json.dumps({"only": args.only, **results[args.only]}))
         return 0
@@ -274,7 +323,7 @@ def main() -> int:
         "config": {"workload": "c2: " + DESC["c2"], "M": 4096, "N": 4096, "K": 4096, "accumulate": "int32"},
         "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK["int8"], "unit": "TOP/s",
                      "frac": head["tflops_frac_peak"], "traffic": traffic,
-                     "kernel": "gemm_mfma_kernel<int8, 256x256, A k-contiguous, B n-contiguous>",
+                     "kernel": "gemm_dma_kernel<int8, 256x256 tile, 2-stage global->LDS DMA, A k-contiguous, B n-contiguous>",
                      "per_launch_ms": head["kernel_ms_mean"]},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "configs": results,
