@@ -193,6 +193,56 @@ def run_vendor(name: str, inp, steps: int, warmup: int) -> dict:
     return res
 
 
+# Element-wise device ops of the backend, on the c3 A operand's shape (134,217,728 elements).
+EW = {
+    "cast_c3a": "typecast bf16 -> fp32 of [16,2048,4096] (the CPU backend's widening of c3's A)",
+    "random_c3a": "seeded uniform bf16 [16,2048,4096] (ops::Random on the device)",
+    "fill_c3a": "fill fp32 [16,2048,4096] with 1.0 (ops::Ones on the device)",
+}
+
+
+def run_ew(name: str, steps: int, warmup: int) -> dict:
+    """HBM-bound element-wise kernels: algorithmic bytes = elements read once + written once."""
+    import torch
+
+    import tensorvia_amd as tv
+    L = tv.lib()
+    n = 16 * 2048 * 4096
+    sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if name == "cast_c3a":
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").view(torch.int16)  # bf16 storage
+        tv.check(L.tv_hip_random(ctypes.c_void_p(src.data_ptr()), tv.BFLOAT16, n, -1.0, 1.0, 5, sh))
+        dst = torch.empty(n, dtype=torch.float32, device="cuda")
+        call = lambda: L.tv_hip_typecast(ctypes.c_void_p(src.data_ptr()), tv.BFLOAT16,  # noqa: E731
+                                         ctypes.c_void_p(dst.data_ptr()), tv.FLOAT32, n, sh)
+        nbytes = n * 2 + n * 4
+    elif name == "random_c3a":
+        dst = torch.empty(n, dtype=torch.int16, device="cuda")
+        call = lambda: L.tv_hip_random(ctypes.c_void_p(dst.data_ptr()), tv.BFLOAT16, n, -1.0, 1.0, 5, sh)  # noqa: E731
+        nbytes = n * 2
+    else:
+        dst = torch.empty(n, dtype=torch.float32, device="cuda")
+        call = lambda: L.tv_hip_fill(ctypes.c_void_p(dst.data_ptr()), tv.FLOAT32, n, 1.0, sh)  # noqa: E731
+        nbytes = n * 4
+    for _ in range(warmup):
+        tv.check(call())
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        call()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    res = {"workload": EW[name], "kernel_ms_mean": ms, "algorithmic_bytes": nbytes,
+           "hbm_gbs": nbytes / (ms * 1e-3) / 1e9}
+    res["hbm_frac_peak"] = res["hbm_gbs"] / PEAK_HBM_GBS
+    del dst
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_copy(steps: int, warmup: int) -> dict:
     """Calibration for the HBM traffic counters: a plain device copy of a known size (512 MiB read,
     512 MiB written per launch; larger than the 256 MB MALL)."""
@@ -251,7 +301,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5m1,c5m8")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5m1,c5m8,cast_c3a,random_c3a,fill_c3a")
     ap.add_argument("--only", default=None,
                     help="run only this config's GPU kernel (for profilers); 'copy' runs the traffic calibration copy")
     ap.add_argument("--no-cpu", action="store_true")
@@ -279,6 +329,11 @@ def main() -> int:
         names.insert(0, "c2")
     results, inputs = {}, {}
     for n in names:
+        if n in EW:
+            log(f"gpu {n}: {EW[n]}")
+            results[n] = run_ew(n, args.steps, args.warmup)
+            log(f"gpu {n}: {results[n]['kernel_ms_mean'] * 1e3:.1f} us  {results[n]['hbm_gbs']:.0f} GB/s")
+            continue
         log(f"gpu {n}: {DESC[n]}")
         results[n], inputs[n] = run_gpu(n, args.steps, args.warmup)
         log(f"gpu {n}: {results[n]['kernel_ms_mean'] * 1e3:.1f} us  {results[n]['tflops']:.1f} T/s  "
@@ -299,7 +354,7 @@ def main() -> int:
         log(f"cpu c2: {cpu['seconds']:.2f} s, {cpu['value'] * 1e3:.1f} GOP/s on {cpu['cores']} threads")
         if args.cpu_all:
             for n in names:
-                if n != "c2":
+                if n != "c2" and n not in EW:
                     log(f"cpu baseline {n}")
                     results[n]["cpu_baseline"] = run_cpu(n, inputs[n], iters=1)
 

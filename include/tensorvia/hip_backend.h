@@ -76,4 +76,24 @@ template <via::Device D> struct MulImpl;
 template <> struct MulImpl<via::Device::HIP> {
     static Tensor execute(const Tensor& a, const Tensor& b);
 };
+
+template <via::Device D> struct TypecastImpl;
+template <via::Device D> struct FillImpl;
+template <via::Device D> struct RandomImpl;
+
+// Element-wise cast on the device (tv_hip_typecast; replaces TypecastImpl<Device::CUDA>,
+// src/backend/cuda/typecast.cu:29+).  Views are made contiguous on the device first.
+template <> struct TypecastImpl<via::Device::HIP> {
+    static Tensor execute(const Tensor& a, via::DataType dst_type);
+};
+// Constant fill on the device (tv_hip_fill; replaces FillImpl/ZerosImpl/OnesImpl<Device::CUDA>,
+// src/backend/cuda/initializer.cu:39-98).
+template <> struct FillImpl<via::Device::HIP> {
+    static Tensor execute(const std::vector<int64_t>& shape, via::DataType dtype, float value);
+};
+// Seeded uniform values generated on the device (tv_hip_random; replaces RandomImpl<Device::CUDA>,
+// src/backend/cuda/initializer.cu:99+), bit-identical to ops::detail::random_fill.
+template <> struct RandomImpl<via::Device::HIP> {
+    static Tensor execute(const std::vector<int64_t>& shape, via::DataType dtype, float min, float max, uint64_t seed);
+};
 } // namespace ops

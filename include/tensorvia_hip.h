@@ -17,6 +17,16 @@
  *                    87-96) that decode-shaped calls (M <= 8) take; no CUDA counterpart exists.
  *   tv_hip_strerror <- the std::runtime_error texts the reference throws (src/ops.cpp:542-556,
  *                    include/backend/cuda/cuda_tensor.cpp:20-23).
+ *   tv_hip_typecast <- TypecastImpl<Device::CUDA>::execute (src/backend/cuda/typecast.cu:7-27,29+),
+ *                    restating the CPU cast (src/backend/cpu/typecast.cpp:48-98) over the pairs of
+ *                    valid_casts (include/core/type_traits.h:237-260).
+ *   tv_hip_fill     <- FillImpl / ZerosImpl / OnesImpl<Device::CUDA> (src/backend/cuda/initializer.cu:16-20,
+ *                    39-98; CPU src/backend/cpu/initializer.cpp:14-17,39-66) behind ops::Fill/Zeros/Ones
+ *                    (src/ops.cpp:85-138).
+ *   tv_hip_random   <- RandomImpl<Device::CUDA> (src/backend/cuda/initializer.cu:22-37,99+; CPU
+ *                    src/backend/cpu/initializer.cpp:18-36,69-77) behind ops::Random (src/ops.cpp:139-156),
+ *                    with a seeded counter-based stream in place of the reference's clock-seeded
+ *                    generators.
  *
  * Semantics (matching the reference CPU backend, src/backend/cpu/mul.cpp:97-145):
  *   C[b, m, n] = sum_k A[b, m, k] * B[b, k, n]
@@ -102,17 +112,34 @@ typedef struct tv_repack_args {
 } tv_repack_args;
 int tv_hip_repack(const tv_repack_args* args, void* hip_stream);
 
+/* Element-wise cast of n contiguous elements, dst[i] = static_cast<dst>(src[i]) with half types
+ * going through their float value (round to nearest even into fp16/bf16, truncation toward zero
+ * into integers).  Serves the pairs of the reference's valid_casts table and same-dtype copies;
+ * any other pair returns TV_E_DTYPE. */
+int tv_hip_typecast(const void* src, int32_t src_dtype, void* dst, int32_t dst_dtype, int64_t n, void* hip_stream);
+
+/* dst[0..n) = static_cast<dtype>(value). */
+int tv_hip_fill(void* dst, int32_t dtype, int64_t n, float value, void* hip_stream);
+
+/* dst[0..n) = elements 0..n-1 of the seeded uniform stream: element i is SplitMix64 output
+ * mix64(mix64(seed + G) + (i + 1) * G), G = 0x9E3779B97F4A7C15.  Integer dtypes take
+ * lo + ((top 32 bits * (hi - lo + 1)) >> 32) in [lo, hi] = [(int64)min, (int64)max]; the others take
+ * min + (max - min) * u in fp32 (no fused multiply-add), u = top 24 bits / 2^24, rounded to the
+ * dtype.  Bit-identical to the host generator for the same (seed, dtype, min, max).  min > max
+ * returns TV_E_SHAPE. */
+int tv_hip_random(void* dst, int32_t dtype, int64_t n, float min, float max, uint64_t seed, void* hip_stream);
+
 /* Human-readable text for any return code of this library. */
 const char* tv_hip_strerror(int code);
 
 /* ABI version of this header (bumped on any change of tv_gemm_args or the entry points). */
 int tv_hip_abi_version(void);
 
-/* Test hook: the next `count` calls of tv_hip_gemm / tv_hip_gemv return `code` without touching
+/* Test hook: the next `count` calls of any compute entry point return `code` without touching
  * the device.  Lets host code prove error propagation without a GPU.  count = 0 disarms. */
 void tv_hip_inject_fault(int code, int count);
 
-#define TV_HIP_ABI_VERSION 2
+#define TV_HIP_ABI_VERSION 3
 
 #ifdef __cplusplus
 }

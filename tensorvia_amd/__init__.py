@@ -27,8 +27,8 @@ TV_OK = 0
 TV_E_NULL, TV_E_SHAPE, TV_E_DTYPE, TV_E_UNSUPPORTED, TV_E_INJECTED, TV_E_NOMEM = -1, -2, -3, -4, -5, -6
 
 # Every symbol include/tensorvia_hip.h declares.
-EXPORTED_SYMBOLS = ("tv_hip_gemm", "tv_hip_gemv", "tv_hip_repack", "tv_hip_strerror", "tv_hip_abi_version",
-                    "tv_hip_inject_fault")
+EXPORTED_SYMBOLS = ("tv_hip_gemm", "tv_hip_gemv", "tv_hip_repack", "tv_hip_typecast", "tv_hip_fill",
+                    "tv_hip_random", "tv_hip_strerror", "tv_hip_abi_version", "tv_hip_inject_fault")
 
 
 class TvGemmArgs(ctypes.Structure):
@@ -77,6 +77,14 @@ def lib() -> ctypes.CDLL:
         L.tv_hip_gemv.restype = ctypes.c_int
         L.tv_hip_repack.argtypes = [ctypes.POINTER(TvRepackArgs), ctypes.c_void_p]
         L.tv_hip_repack.restype = ctypes.c_int
+        L.tv_hip_typecast.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                                      ctypes.c_int64, ctypes.c_void_p]
+        L.tv_hip_typecast.restype = ctypes.c_int
+        L.tv_hip_fill.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p]
+        L.tv_hip_fill.restype = ctypes.c_int
+        L.tv_hip_random.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_float,
+                                    ctypes.c_uint64, ctypes.c_void_p]
+        L.tv_hip_random.restype = ctypes.c_int
         L.tv_hip_strerror.argtypes = [ctypes.c_int]
         L.tv_hip_strerror.restype = ctypes.c_char_p
         L.tv_hip_abi_version.argtypes = []

@@ -28,7 +28,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 KERNEL_SOURCES = ["gemm_mfma_f32.hip", "gemm_mfma_bf16.hip", "gemm_mfma_f16.hip", "gemm_mfma_i8.hip",
-                  "gemm_dispatch.hip", "gemv.hip", "gemm_simt.hip", "repack.hip", "capi.hip"]
+                  "gemm_dispatch.hip", "gemv.hip", "gemm_simt.hip", "repack.hip", "elementwise.hip", "capi.hip"]
 
 
 def _run(cmd: list[str], verbose: bool) -> None:

@@ -135,6 +135,39 @@ int tv_hip_repack(const tv_repack_args* args, void* hip_stream) {
     return tvk::launch_repack(args, static_cast<hipStream_t>(hip_stream));
 }
 
+int tv_hip_typecast(const void* src, int32_t src_dtype, void* dst, int32_t dst_dtype, int64_t n, void* hip_stream) {
+    int code;
+    if (take_fault(&code)) return code;
+    if (src_dtype < TV_INT8 || src_dtype > TV_FLOAT64 || dst_dtype < TV_INT8 || dst_dtype > TV_FLOAT64) return TV_E_DTYPE;
+    if (n < 0) return TV_E_SHAPE;
+    if (n == 0) return TV_OK;
+    if (!src || !dst) return TV_E_NULL;
+    hipStream_t s = static_cast<hipStream_t>(hip_stream);
+    if (src_dtype == dst_dtype)
+        return hipMemcpyAsync(dst, src, (size_t)n * tvk::dtype_size(src_dtype), hipMemcpyDeviceToDevice, s);
+    return tvk::launch_typecast(src, src_dtype, dst, dst_dtype, n, s);
+}
+
+int tv_hip_fill(void* dst, int32_t dtype, int64_t n, float value, void* hip_stream) {
+    int code;
+    if (take_fault(&code)) return code;
+    if (dtype < TV_INT8 || dtype > TV_FLOAT64) return TV_E_DTYPE;
+    if (n < 0) return TV_E_SHAPE;
+    if (n == 0) return TV_OK;
+    if (!dst) return TV_E_NULL;
+    return tvk::launch_fill(dst, dtype, n, value, static_cast<hipStream_t>(hip_stream));
+}
+
+int tv_hip_random(void* dst, int32_t dtype, int64_t n, float min, float max, uint64_t seed, void* hip_stream) {
+    int code;
+    if (take_fault(&code)) return code;
+    if (dtype < TV_INT8 || dtype > TV_FLOAT64) return TV_E_DTYPE;
+    if (n < 0 || !(min <= max)) return TV_E_SHAPE;
+    if (n == 0) return TV_OK;
+    if (!dst) return TV_E_NULL;
+    return tvk::launch_random(dst, dtype, n, min, max, seed, static_cast<hipStream_t>(hip_stream));
+}
+
 const char* tv_hip_strerror(int code) {
     switch (code) {
         case TV_OK: return "success";

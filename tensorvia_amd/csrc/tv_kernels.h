@@ -42,6 +42,9 @@ enum LoadMode : int {
 int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream);
 int launch_gemm_simt(const GemmDesc& d, hipStream_t stream);
 int launch_repack(const tv_repack_args* a, hipStream_t stream);
+int launch_typecast(const void* src, int src_dt, void* dst, int dst_dt, int64_t n, hipStream_t stream);
+int launch_fill(void* dst, int dt, int64_t n, float value, hipStream_t stream);
+int launch_random(void* dst, int dt, int64_t n, float min, float max, uint64_t seed, hipStream_t stream);
 int launch_gemv(const GemmDesc& d, hipStream_t stream); // TV_E_UNSUPPORTED if it does not serve d
 // GEMV with an explicit strip width (nl lanes), workgroup size and K split (tuning sweeps).
 int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices);

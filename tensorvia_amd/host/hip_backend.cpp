@@ -220,4 +220,38 @@ Tensor MulImpl<Device::HIP>::execute(const Tensor& a, const Tensor& b) {
     return c;
 }
 
+// ---- TypecastImpl / FillImpl / RandomImpl<HIP> ---------------------------------------------------
+
+Tensor TypecastImpl<Device::HIP>::execute(const Tensor& a, DataType dst_type) {
+    const Tensor src = a.contiguous(); // device repack of a view; a dense tensor is shared as is
+    Tensor out(src.shape(), dst_type, Device::HIP);
+    auto ctx = hip_ctx_of(out.get_impl());
+    const char* sp = static_cast<const char*>(src.data()) + src.offset() * calc_dtype_size(src.dtype());
+    tv_check(tv_hip_typecast(sp, static_cast<int32_t>(src.dtype()), out.data(), static_cast<int32_t>(dst_type),
+                             static_cast<int64_t>(src.numel()), ctx->stream()),
+             "ops::Typecast");
+    ctx->wait();
+    return out;
+}
+
+Tensor FillImpl<Device::HIP>::execute(const std::vector<int64_t>& shape, DataType dtype, float value) {
+    Tensor out(shape, dtype, Device::HIP);
+    auto ctx = hip_ctx_of(out.get_impl());
+    tv_check(tv_hip_fill(out.data(), static_cast<int32_t>(dtype), static_cast<int64_t>(out.numel()), value, ctx->stream()),
+             "ops::Fill");
+    ctx->wait();
+    return out;
+}
+
+Tensor RandomImpl<Device::HIP>::execute(const std::vector<int64_t>& shape, DataType dtype, float min, float max,
+                                        uint64_t seed) {
+    Tensor out(shape, dtype, Device::HIP);
+    auto ctx = hip_ctx_of(out.get_impl());
+    tv_check(tv_hip_random(out.data(), static_cast<int32_t>(dtype), static_cast<int64_t>(out.numel()), min, max, seed,
+                           ctx->stream()),
+             "ops::Random");
+    ctx->wait();
+    return out;
+}
+
 } // namespace ops

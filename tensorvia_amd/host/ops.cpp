@@ -75,19 +75,23 @@ Tensor cast_tensor(const Tensor& a, DataType dst) {
 }
 } // namespace
 
+// Validation as the reference's (src/ops.cpp:1277-1300); device tensors cast on the device,
+// host tensors on the host.
 Tensor Typecast(const Tensor& a, DataType dst_type) {
     if (a.numel() == 0) throw std::runtime_error("tensor a is null");
     if (!is_cast_valid(a.dtype(), dst_type))
         throw std::runtime_error("Invalid typecast from " + std::string(dtype_to_string(a.dtype())) + " to " +
                                  std::string(dtype_to_string(dst_type)));
     if (a.dtype() == dst_type) return a;
+    if (a.device() == Device::HIP) return TypecastImpl<Device::HIP>::execute(a, dst_type);
     return cast_tensor(a, dst_type);
 }
 
 void Typecast(Tensor& a, DataType dst_type) { a = Typecast(static_cast<const Tensor&>(a), dst_type); }
 
 // ---- initialisers ------------------------------------------------------------------------------
-// Values are produced on the host in the tensor's element type and copied to the device once.
+// Values are produced on the device (tv_hip_fill / tv_hip_random).  The host generator below
+// (detail::random_fill) produces the same stream for host buffers.
 
 namespace {
 constexpr uint64_t kGamma = 0x9E3779B97F4A7C15ull;
@@ -97,27 +101,21 @@ inline uint64_t mix64(uint64_t z) {
     return z ^ (z >> 31);
 }
 
-Tensor host_filled(const std::vector<int64_t>& shape, DataType dtype, const std::function<void(void*, size_t)>& fill) {
-    Tensor t(shape, dtype, Device::CPU);
-    fill(t.data(), t.numel());
-    t.to_device();
-    return t;
-}
-
 uint64_t g_next_seed = 0x5EEDull;
 } // namespace
 
 Tensor Fill(const std::vector<int64_t>& shape, DataType dtype, float value) {
-    return host_filled(shape, dtype, [&](void* p, size_t n) {
-        dispatch_dtype(dtype, [&](auto id) {
-            using E = typename decltype(id)::type;
-            E* e = static_cast<E*>(p);
-            for (size_t i = 0; i < n; ++i) e[i] = static_cast<E>(value);
-        });
-    });
+    if (shape.empty()) throw std::runtime_error("ops::Fill: shape is empty");
+    return FillImpl<Device::HIP>::execute(shape, dtype, value);
 }
-Tensor Zeros(const std::vector<int64_t>& shape, DataType dtype) { return Fill(shape, dtype, 0.0f); }
-Tensor Ones(const std::vector<int64_t>& shape, DataType dtype) { return Fill(shape, dtype, 1.0f); }
+Tensor Zeros(const std::vector<int64_t>& shape, DataType dtype) {
+    if (shape.empty()) throw std::runtime_error("ops::Zeros: shape is empty");
+    return FillImpl<Device::HIP>::execute(shape, dtype, 0.0f);
+}
+Tensor Ones(const std::vector<int64_t>& shape, DataType dtype) {
+    if (shape.empty()) throw std::runtime_error("ops::Ones: shape is empty");
+    return FillImpl<Device::HIP>::execute(shape, dtype, 1.0f);
+}
 
 // Counter-based SplitMix64 stream: element i of stream `seed` is mix64(mix64(seed + G) + (i+1) G).
 // Reals: min + (max - min) * u in fp32, u = top 24 bits / 2^24, then rounded to the element type
@@ -149,8 +147,9 @@ void random_fill(void* p, size_t n, DataType dtype, float min, float max, uint64
 } // namespace detail
 
 Tensor Random(const std::vector<int64_t>& shape, DataType dtype, float min, float max, uint64_t seed) {
+    if (shape.empty()) throw std::runtime_error("ops::Random: shape is empty");
     if (min > max) throw std::runtime_error("Random: min must not exceed max");
-    return host_filled(shape, dtype, [&](void* p, size_t n) { detail::random_fill(p, n, dtype, min, max, seed); });
+    return RandomImpl<Device::HIP>::execute(shape, dtype, min, max, seed);
 }
 
 Tensor Random(const std::vector<int64_t>& shape, DataType dtype, float min, float max) {

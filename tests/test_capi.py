@@ -87,6 +87,33 @@ def test_rejections(fn):
     assert _call(fn, _args(batch=0)) == tv.TV_OK
 
 
+def test_elementwise_rejections():
+    """Typecast / fill / random reject bad arguments before any launch, and n = 0 is a no-op."""
+    L = tv.lib()
+    p = ctypes.c_void_p(64)  # never dereferenced
+    assert L.tv_hip_typecast(p, 9, p, tv.FLOAT32, 4, None) == tv.TV_E_DTYPE
+    assert L.tv_hip_typecast(p, tv.INT8, p, -1, 4, None) == tv.TV_E_DTYPE
+    assert L.tv_hip_typecast(p, tv.INT8, p, tv.BFLOAT16, 4, None) == tv.TV_E_DTYPE  # not in valid_casts
+    assert L.tv_hip_typecast(p, tv.FLOAT64, p, tv.FLOAT16, 4, None) == tv.TV_E_DTYPE
+    assert L.tv_hip_typecast(p, tv.INT8, p, tv.FLOAT32, -1, None) == tv.TV_E_SHAPE
+    assert L.tv_hip_typecast(None, tv.INT8, p, tv.FLOAT32, 4, None) == tv.TV_E_NULL
+    assert L.tv_hip_typecast(None, tv.INT8, None, tv.FLOAT32, 0, None) == tv.TV_OK
+    assert L.tv_hip_fill(p, 8, 4, 1.0, None) == tv.TV_E_DTYPE
+    assert L.tv_hip_fill(p, tv.INT8, -3, 1.0, None) == tv.TV_E_SHAPE
+    assert L.tv_hip_fill(None, tv.INT8, 3, 1.0, None) == tv.TV_E_NULL
+    assert L.tv_hip_fill(None, tv.INT8, 0, 1.0, None) == tv.TV_OK
+    assert L.tv_hip_random(p, -2, 4, 0.0, 1.0, 1, None) == tv.TV_E_DTYPE
+    assert L.tv_hip_random(p, tv.FLOAT32, 4, 2.0, 1.0, 1, None) == tv.TV_E_SHAPE  # min > max
+    assert L.tv_hip_random(p, tv.FLOAT32, -1, 0.0, 1.0, 1, None) == tv.TV_E_SHAPE
+    assert L.tv_hip_random(None, tv.FLOAT32, 4, 0.0, 1.0, 1, None) == tv.TV_E_NULL
+    assert L.tv_hip_random(None, tv.FLOAT32, 0, 0.0, 1.0, 1, None) == tv.TV_OK
+    L.tv_hip_inject_fault(tv.TV_E_INJECTED, 3)
+    assert L.tv_hip_typecast(p, tv.INT8, p, tv.FLOAT32, 4, None) == tv.TV_E_INJECTED
+    assert L.tv_hip_fill(p, tv.INT8, 4, 1.0, None) == tv.TV_E_INJECTED
+    assert L.tv_hip_random(p, tv.INT8, 4, 0.0, 1.0, 1, None) == tv.TV_E_INJECTED
+    L.tv_hip_inject_fault(0, 0)
+
+
 def test_gemv_rejects_large_m_and_non_mfma_pairs():
     assert _call("tv_hip_gemv", _args(M=9)) == tv.TV_E_UNSUPPORTED
     assert _call("tv_hip_gemv", _args(dtype_a=tv.INT32, dtype_b=tv.INT32, dtype_c=tv.INT32)) == tv.TV_E_UNSUPPORTED
