@@ -8,6 +8,7 @@
 #include <memory>
 
 #include "context.h"
+#include "ops.h"
 #include "tensor.h"
 
 // One HIP device (the one with the most memory, as CUDAContext picks, cuda_context.h:14-36) and
@@ -75,6 +76,12 @@ template <via::Device D> struct MulImpl;
 // src/backend/cuda/mul.cu:52-124).
 template <> struct MulImpl<via::Device::HIP> {
     static Tensor execute(const Tensor& a, const Tensor& b);
+};
+
+template <via::Device D> struct MulBiasActImpl;
+// The fused matmul + bias + activation (tv_hip_gemm_ex).
+template <> struct MulBiasActImpl<via::Device::HIP> {
+    static Tensor execute(const Tensor& a, const Tensor& b, const Tensor* bias, Activation act);
 };
 
 template <via::Device D> struct TypecastImpl;

@@ -19,6 +19,14 @@ OPS_API Tensor Mul(const Tensor& a, const Tensor& b);
 // Spelling used by the reference README (README.md:116); same operation.
 OPS_API Tensor matmul(const Tensor& a, const Tensor& b);
 
+// Beyond the reference: act(Mul(a, b) + bias) in one pass, the bias added and the activation
+// applied to the fp32 accumulator before the single rounding to the result dtype (the reference
+// composes ops::Mul, ops::Add and ops::Relu/Silu/Tanh/Sigmoid, src/ops.cpp:330-352, 678-780).
+// bias: nullptr, or a tensor of the result dtype shaped [n], [m, n] or [b, m, n] (broadcast over
+// the missing leading dimensions).  Float results only (fp32, bf16, fp16 inputs).
+enum class Activation { None = 0, Relu = 1, Silu = 2, Sigmoid = 3, Tanh = 4 };
+OPS_API Tensor MulBiasAct(const Tensor& a, const Tensor& b, const Tensor* bias, Activation act);
+
 // Materialising N-d transpose (reference src/ops.cpp:1380-1402).
 OPS_API Tensor Transpose(const Tensor& a, std::initializer_list<int64_t> axes);
 OPS_API void Transpose(Tensor& a); // 2-d, in place

@@ -15,6 +15,10 @@
  *                    operands are consumed without a repack.
  *   tv_hip_gemv   <- the batch*M*N < 2^20 "basic" branch of mul_kernel (src/backend/cpu/mul.cpp:7-25,
  *                    87-96) that decode-shaped calls (M <= 8) take; no CUDA counterpart exists.
+ *   tv_hip_gemm_ex <- ops::Mul followed by ops::Add(C, bias) (src/ops.cpp:330-352,
+ *                    src/backend/cpu/arithmetic.cpp:308-330) and ops::Relu / Silu / Sigmoid / Tanh
+ *                    (src/backend/cpu/activate.cpp:8-40, src/backend/cuda/activate.cu:8-36), fused
+ *                    into the matmul's epilogue; no single reference function does this.
  *   tv_hip_strerror <- the std::runtime_error texts the reference throws (src/ops.cpp:542-556,
  *                    include/backend/cuda/cuda_tensor.cpp:20-23).
  *   tv_hip_typecast <- TypecastImpl<Device::CUDA>::execute (src/backend/cuda/typecast.cu:7-27,29+),
@@ -91,6 +95,31 @@ typedef struct tv_gemm_args {
  * dtype/layout, everything else to the MFMA GEMM kernels (or the SIMT slow path). */
 int tv_hip_gemm(const tv_gemm_args* args, void* hip_stream);
 
+/* Activations of the fused epilogue (the reference's ops::Relu / Silu / Sigmoid / Tanh). */
+enum tv_act {
+    TV_ACT_NONE = 0,
+    TV_ACT_RELU = 1,    /* x > 0 ? x : 0 */
+    TV_ACT_SILU = 2,    /* x / (1 + exp(-x)) */
+    TV_ACT_SIGMOID = 3, /* 1 / (1 + exp(-x)) */
+    TV_ACT_TANH = 4     /* tanh(x) */
+};
+
+/* Fused epilogue: C[b, m, n] = act(sum_k A*B + bias[b, m, n]), computed on the fp32 accumulator and
+ * rounded once to dtype_c.  Element (b, m, n) of the bias lives at bias + b*sbias_b + m*sbias_m +
+ * n*sbias_n (element units, dtype = dtype_c); zero strides broadcast (sbias_b = sbias_m = 0,
+ * sbias_n = 1 is a per-column bias vector).  bias = NULL adds nothing. */
+typedef struct tv_epilogue {
+    int32_t act;        /* enum tv_act */
+    int32_t reserved;   /* must be 0 */
+    const void* bias;
+    int64_t sbias_b, sbias_m, sbias_n;
+} tv_epilogue;
+
+/* tv_hip_gemm with a fused epilogue (ep = NULL: same as tv_hip_gemm).  Served for the float-output
+ * matrix-core pairs (fp32 -> fp32, bf16 -> bf16/fp32, fp16 -> fp16/fp32); integer outputs return
+ * TV_E_UNSUPPORTED, an act outside enum tv_act TV_E_UNSUPPORTED. */
+int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_stream);
+
 /* Skinny-M (M <= 8) matrix-vector path: HBM-streaming, no matrix cores.  Returns
  * TV_E_UNSUPPORTED for M > 8 or for a dtype pair it does not serve. */
 int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream);
@@ -139,7 +168,7 @@ int tv_hip_abi_version(void);
  * the device.  Lets host code prove error propagation without a GPU.  count = 0 disarms. */
 void tv_hip_inject_fault(int code, int count);
 
-#define TV_HIP_ABI_VERSION 3
+#define TV_HIP_ABI_VERSION 4
 
 #ifdef __cplusplus
 }

@@ -27,7 +27,7 @@ TV_OK = 0
 TV_E_NULL, TV_E_SHAPE, TV_E_DTYPE, TV_E_UNSUPPORTED, TV_E_INJECTED, TV_E_NOMEM = -1, -2, -3, -4, -5, -6
 
 # Every symbol include/tensorvia_hip.h declares.
-EXPORTED_SYMBOLS = ("tv_hip_gemm", "tv_hip_gemv", "tv_hip_repack", "tv_hip_typecast", "tv_hip_fill",
+EXPORTED_SYMBOLS = ("tv_hip_gemm", "tv_hip_gemm_ex", "tv_hip_gemv", "tv_hip_repack", "tv_hip_typecast", "tv_hip_fill",
                     "tv_hip_random", "tv_hip_strerror", "tv_hip_abi_version", "tv_hip_inject_fault")
 
 
@@ -42,6 +42,17 @@ class TvGemmArgs(ctypes.Structure):
         ("B", ctypes.c_void_p), ("sb_b", ctypes.c_int64), ("sb_k", ctypes.c_int64), ("sb_n", ctypes.c_int64),
         ("C", ctypes.c_void_p), ("sc_b", ctypes.c_int64), ("sc_m", ctypes.c_int64), ("sc_n", ctypes.c_int64),
     ]
+
+
+# enum tv_act
+ACT_NONE, ACT_RELU, ACT_SILU, ACT_SIGMOID, ACT_TANH = range(5)
+
+
+class TvEpilogue(ctypes.Structure):
+    """Mirror of ``tv_epilogue`` (include/tensorvia_hip.h)."""
+
+    _fields_ = [("act", ctypes.c_int32), ("reserved", ctypes.c_int32), ("bias", ctypes.c_void_p),
+                ("sbias_b", ctypes.c_int64), ("sbias_m", ctypes.c_int64), ("sbias_n", ctypes.c_int64)]
 
 
 TV_MAX_DIMS = 8
@@ -73,6 +84,8 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(str(KERNEL_LIB))
         L.tv_hip_gemm.argtypes = [ctypes.POINTER(TvGemmArgs), ctypes.c_void_p]
         L.tv_hip_gemm.restype = ctypes.c_int
+        L.tv_hip_gemm_ex.argtypes = [ctypes.POINTER(TvGemmArgs), ctypes.POINTER(TvEpilogue), ctypes.c_void_p]
+        L.tv_hip_gemm_ex.restype = ctypes.c_int
         L.tv_hip_gemv.argtypes = [ctypes.POINTER(TvGemmArgs), ctypes.c_void_p]
         L.tv_hip_gemv.restype = ctypes.c_int
         L.tv_hip_repack.argtypes = [ctypes.POINTER(TvRepackArgs), ctypes.c_void_p]

@@ -74,8 +74,24 @@ int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
     d->sc_b = a->sc_b; d->sc_m = a->sc_m; d->sc_n = a->sc_n;
     d->M = (int32_t)a->M; d->N = (int32_t)a->N; d->K = (int32_t)a->K; d->batch = (int32_t)a->batch;
     d->dtype_a = a->dtype_a; d->dtype_b = a->dtype_b; d->dtype_c = a->dtype_c;
+    d->bias = nullptr;
+    d->sbias_b = d->sbias_m = d->sbias_n = 0;
+    d->act = TV_ACT_NONE;
     (void)is_float_dt;
     return TV_OK;
+}
+
+// Routing shared by tv_hip_gemm and tv_hip_gemm_ex.
+int run_gemm(const tv_gemm_args* args, const tvk::GemmDesc& d, hipStream_t s) {
+    if (d.batch == 0 || d.M == 0 || d.N == 0) return TV_OK;
+    if (mfma_pair(args)) {
+        if (d.M <= 8) {
+            const int rc = tvk::launch_gemv(d, s);
+            if (rc != TV_E_UNSUPPORTED) return rc;
+        }
+        return tvk::launch_gemm_mfma(d, s);
+    }
+    return tvk::launch_gemm_simt(d, s);
 }
 
 } // namespace
@@ -95,16 +111,26 @@ int tv_hip_gemm(const tv_gemm_args* args, void* hip_stream) {
     tvk::GemmDesc d;
     int rc = validate(args, &d);
     if (rc) return rc;
-    if (d.batch == 0 || d.M == 0 || d.N == 0) return TV_OK;
-    hipStream_t s = static_cast<hipStream_t>(hip_stream);
-    if (mfma_pair(args)) {
-        if (d.M <= 8) {
-            rc = tvk::launch_gemv(d, s);
-            if (rc != TV_E_UNSUPPORTED) return rc;
-        }
-        return tvk::launch_gemm_mfma(d, s);
+    return run_gemm(args, d, static_cast<hipStream_t>(hip_stream));
+}
+
+int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_stream) {
+    int code;
+    if (take_fault(&code)) return code;
+    tvk::GemmDesc d;
+    int rc = validate(args, &d);
+    if (rc) return rc;
+    if (ep) {
+        if (ep->act < TV_ACT_NONE || ep->act > TV_ACT_TANH || ep->reserved != 0) return TV_E_UNSUPPORTED;
+        const bool float_out = args->dtype_c == TV_FLOAT32 || args->dtype_c == TV_BFLOAT16 || args->dtype_c == TV_FLOAT16;
+        if (!mfma_pair(args) || !float_out) return TV_E_UNSUPPORTED;
+        d.bias = ep->bias;
+        d.sbias_b = ep->sbias_b;
+        d.sbias_m = ep->sbias_m;
+        d.sbias_n = ep->sbias_n;
+        d.act = ep->act;
     }
-    return tvk::launch_gemm_simt(d, s);
+    return run_gemm(args, d, static_cast<hipStream_t>(hip_stream));
 }
 
 int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream) {

@@ -308,6 +308,9 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
     // load into LDS is left in flight when the workgroup ends); all waves leave the k-loop's LDS
     // before any wave stages its output there.
     wait_vmcnt<0>();
+    if constexpr (!__is_same(Acc, i32x4))
+        if (has_epilogue(d))
+            apply_epilogue<C>(acc, d, b, m0 + wm * C::WM + (lane & 15), n0 + wn * C::WN + (lane >> 4) * 4);
     const size_t csz = dtype_size(d.dtype_c);
     char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
     if (c_vec == 2) {
@@ -488,6 +491,10 @@ void gemm_smallk_kernel(GemmDesc d, int tiles_m, int tiles_n) {
                     for (int j = 0; j < C::FN; ++j) Op::run(fb[j], fa[i], acc[i][j]);
             }
         }
+        // The fused epilogue reads its bias before the next tile's loads are issued.
+        if constexpr (!__is_same(Acc, i32x4))
+            if (has_epilogue(d))
+                apply_epilogue<C>(acc, d, b, m0 + wm * C::WM + (lane & 15), n0 + wn * C::WN + (lane >> 4) * 4);
         dma_barrier(); // every wave is done reading the operands
         const int cb = b, cm0 = m0, cn0 = n0;
         const int next = t + 1;

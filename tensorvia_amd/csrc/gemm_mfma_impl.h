@@ -279,6 +279,23 @@ struct GemmCfg {
 // wrap), the reference CPU backend's int8 result; half outputs round to nearest even.
 template <typename TC, typename V> __device__ inline TC cvt_out(V v) { return static_cast<TC>(v); }
 
+// Fused epilogue on the wave's fp32 accumulators, in place: acc[i][j][q] is C[row0 + 16i][col0 + 16j
+// + q] of batch b.  Positions outside C keep their (unused) values.
+template <class C>
+__device__ inline void apply_epilogue(f32x4 (&acc)[C::FM][C::FN], const GemmDesc& d, int b, int row0, int col0) {
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) {
+        const int row = row0 + 16 * i;
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int col = col0 + 16 * j + q;
+                if (row < d.M && col < d.N) acc[i][j][q] = epilogue_value(acc[i][j][q], d, b, row, col);
+            }
+    }
+}
+
 // Store the wave's accumulators as TC: acc[i][j][q] is C[row0 + 16i][col0 + 16j + q] (the lane's
 // row and first column are folded into row0 / col0), four consecutive columns per vector store.
 template <typename TC, class C, typename Acc>
@@ -535,6 +552,8 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
     const int row0 = m0 + wm * C::WM + (lane & 15);
     const int col0 = n0 + wn * C::WN + (lane >> 4) * 4;
     const bool vec_ok = c_vec != 0;
+    if constexpr (!__is_same(Acc, i32x4))
+        if (has_epilogue(d)) apply_epilogue<C>(acc, d, b, row0, col0);
     if (c_vec == 2) {
         // All waves are done with the k-loop's LDS stages before any wave reuses them.
         lds_barrier();

@@ -124,6 +124,13 @@ __device__ inline void gemv_group(const u32x4 (&w)[kGemvGroupRows], const char* 
     }
 }
 
+// Output value of C[b, m, n] through the fused epilogue (float accumulators only).
+template <typename Acc> __device__ inline Acc gemv_epilogue(Acc v, const GemmDesc& d, int b, int m, int n) {
+    if constexpr (__is_same(Acc, float))
+        if (has_epilogue(d)) return epilogue_value(v, d, b, m, n);
+    return v;
+}
+
 template <typename Acc>
 __device__ inline void gemv_store(void* C, int64_t idx, int dtype_c, Acc v) {
     if constexpr (__is_same(Acc, int)) {
@@ -258,7 +265,9 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
         if (writer)
 #pragma unroll
             for (int m = 0; m < MR; ++m)
-                if (m < d.M) gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + oc) * d.sc_n, d.dtype_c, v[m]);
+                if (m < d.M)
+                    gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + oc) * d.sc_n, d.dtype_c,
+                               gemv_epilogue(v[m], d, b, m, n0 + oc));
         return;
     }
 
@@ -288,7 +297,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
 #pragma unroll
             for (int k = 1; k < kGemvMaxSlices; ++k)
                 if (k < g.nslices) t += part_v[k];
-            gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + c) * d.sc_n, d.dtype_c, t);
+            gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + c) * d.sc_n, d.dtype_c, gemv_epilogue(t, d, b, m, n0 + c));
         }
     }
     if (tid == 0) __hip_atomic_store(g.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

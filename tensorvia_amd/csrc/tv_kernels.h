@@ -28,7 +28,40 @@ struct GemmDesc {
     int64_t sc_b, sc_m, sc_n;
     int32_t M, N, K, batch;
     int32_t dtype_a, dtype_b, dtype_c;
+    // Fused epilogue (float outputs): C = act(acc + bias[b, m, n]) on the fp32 accumulator, rounded
+    // once to dtype_c.  bias == nullptr: no bias; act == TV_ACT_NONE: identity.
+    const void* bias;                  // element type dtype_c
+    int64_t sbias_b, sbias_m, sbias_n; // element strides (0 broadcasts)
+    int32_t act;
 };
+
+__device__ inline bool has_epilogue(const GemmDesc& d) { return d.bias != nullptr || d.act != TV_ACT_NONE; }
+
+// The reference's activations on float values (src/backend/cpu/activate.cpp:8-40,
+// src/backend/cuda/activate.cu:8-36): relu x > 0 ? x : 0, silu x / (1 + exp(-x)),
+// sigmoid 1 / (1 + exp(-x)), tanh.
+__device__ inline float act_apply(float x, int act) {
+    switch (act) {
+        case TV_ACT_RELU: return x > 0.0f ? x : 0.0f;
+        case TV_ACT_SILU: return x / (1.0f + expf(-x));
+        case TV_ACT_SIGMOID: return 1.0f / (1.0f + expf(-x));
+        case TV_ACT_TANH: return tanhf(x);
+        default: return x;
+    }
+}
+
+__device__ inline float bias_at(const GemmDesc& d, int64_t b, int64_t m, int64_t n) {
+    const int64_t i = b * d.sbias_b + m * d.sbias_m + n * d.sbias_n;
+    if (d.dtype_c == TV_BFLOAT16) return (float)static_cast<const __bf16*>(d.bias)[i];
+    if (d.dtype_c == TV_FLOAT16) return (float)static_cast<const _Float16*>(d.bias)[i];
+    return static_cast<const float*>(d.bias)[i];
+}
+
+// One output value through the epilogue (m, n inside C).
+__device__ inline float epilogue_value(float v, const GemmDesc& d, int64_t b, int64_t m, int64_t n) {
+    if (d.bias) v += bias_at(d, b, m, n);
+    return act_apply(v, d.act);
+}
 
 // Operand load modes for one GEMM operand (A: rows m, B: rows n; "K-contiguous" means the
 // reduction index has stride 1).

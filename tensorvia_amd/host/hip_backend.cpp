@@ -184,7 +184,9 @@ struct HIPRegistrar {
 
 namespace ops {
 
-Tensor MulImpl<Device::HIP>::execute(const Tensor& a, const Tensor& b) {
+namespace {
+// Output tensor plus the C-ABI descriptor of a @ b (views through their strides and offsets).
+Tensor pack_gemm(const Tensor& a, const Tensor& b, tv_gemm_args& args) {
     const bool a3 = a.dims() == 3, b3 = b.dims() == 3;
     const int64_t batch = a3 ? a.shape(0) : 1;
     const int64_t M = a.shape(-2), K = a.shape(-1), N = b.shape(-1);
@@ -193,7 +195,7 @@ Tensor MulImpl<Device::HIP>::execute(const Tensor& a, const Tensor& b) {
     Tensor c(shape, res, Device::HIP);
 
     const std::vector<int64_t> sa = a.strides(), sb = b.strides(), sc = c.strides();
-    tv_gemm_args args{};
+    args = tv_gemm_args{};
     args.dtype_a = static_cast<int32_t>(a.dtype());
     args.dtype_b = static_cast<int32_t>(b.dtype());
     args.dtype_c = static_cast<int32_t>(res);
@@ -213,10 +215,48 @@ Tensor MulImpl<Device::HIP>::execute(const Tensor& a, const Tensor& b) {
     args.sc_b = a3 ? sc[0] : 0;
     args.sc_m = sc[a3 ? 1 : 0];
     args.sc_n = sc[a3 ? 2 : 1];
+    return c;
+}
+} // namespace
 
+Tensor MulImpl<Device::HIP>::execute(const Tensor& a, const Tensor& b) {
+    tv_gemm_args args{};
+    Tensor c = pack_gemm(a, b, args);
     auto ctx = hip_ctx_of(c.get_impl());
     tv_check(tv_hip_gemm(&args, ctx->stream()), "ops::Mul");
     ctx->wait(); // the reference's op is synchronous (src/backend/cuda/mul.cu:122)
+    return c;
+}
+
+Tensor MulBiasActImpl<Device::HIP>::execute(const Tensor& a, const Tensor& b, const Tensor* bias, Activation act) {
+    tv_gemm_args args{};
+    Tensor c = pack_gemm(a, b, args);
+    tv_epilogue ep{};
+    ep.act = static_cast<int32_t>(act);
+    if (bias) {
+        if (bias->device() != Device::HIP) throw std::runtime_error("MulBiasAct: bias must be on the HIP device");
+        if (bias->dtype() != c.dtype())
+            throw std::runtime_error("MulBiasAct: bias dtype must be the result dtype " +
+                                     std::string(dtype_to_string(c.dtype())));
+        // Align the bias's dimensions with C's trailing ones; missing leading dimensions broadcast.
+        const size_t cd = c.dims(), bd = bias->dims();
+        if (bd < 1 || bd > cd) throw std::runtime_error("MulBiasAct: bias must have 1 to rank(C) dimensions");
+        const std::vector<int64_t> st = bias->strides();
+        int64_t s3[3] = {0, 0, 0}; // batch, m, n strides of C's [b?, m, n]
+        for (size_t i = 0; i < bd; ++i) {
+            const size_t ci = cd - bd + i;
+            if (bias->shape(i) != c.shape(ci))
+                throw std::runtime_error("MulBiasAct: bias shape does not match the result's trailing dimensions");
+            s3[3 - cd + ci] = bias->shape(i) == 1 ? 0 : st[i];
+        }
+        ep.bias = static_cast<const char*>(bias->data()) + bias->offset() * calc_dtype_size(bias->dtype());
+        ep.sbias_b = s3[0];
+        ep.sbias_m = s3[1];
+        ep.sbias_n = s3[2];
+    }
+    auto ctx = hip_ctx_of(c.get_impl());
+    tv_check(tv_hip_gemm_ex(&args, &ep, ctx->stream()), "ops::MulBiasAct");
+    ctx->wait();
     return c;
 }
 

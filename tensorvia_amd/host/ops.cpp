@@ -12,7 +12,8 @@ namespace ops {
 
 // Validation restates the reference's (src/ops.cpp:540-556) with one extension: a rank-3 A may
 // multiply a rank-2 B (B broadcast over the batch), which the reference rejects.
-Tensor Mul(const Tensor& a, const Tensor& b) {
+namespace {
+void check_mul_operands(const Tensor& a, const Tensor& b) {
     if (a.device() != b.device()) throw std::runtime_error("Tensors a and b device mismatch!");
     const size_t ra = a.dims(), rb = b.dims();
     if (ra != 2 && ra != 3) throw std::runtime_error("Tensors a and b dims must be 2 or 3,but got " + std::to_string(ra));
@@ -27,10 +28,20 @@ Tensor Mul(const Tensor& a, const Tensor& b) {
     if (a.device() == Device::CPU)
         throw std::runtime_error("ops::Mul on CPU tensors runs the reference CPU backend, which is not part of the "
                                  "HIP build; move both tensors with to_device()");
+}
+} // namespace
+
+Tensor Mul(const Tensor& a, const Tensor& b) {
+    check_mul_operands(a, b);
     return MulImpl<Device::HIP>::execute(a, b);
 }
 
 Tensor matmul(const Tensor& a, const Tensor& b) { return Mul(a, b); }
+
+Tensor MulBiasAct(const Tensor& a, const Tensor& b, const Tensor* bias, Activation act) {
+    check_mul_operands(a, b);
+    return MulBiasActImpl<Device::HIP>::execute(a, b, bias, act);
+}
 
 Tensor transpose(const Tensor& a, std::initializer_list<int64_t> axes) {
     if (a.dims() != axes.size()) throw std::runtime_error("transpose shape and axes size not match");

@@ -9,6 +9,11 @@
 //   cast_<s>_<d>     ops::Typecast(ops::Random({257, 33}, s, lo, hi, seed 70 + 8 s + d).t(), d)
 //                    (a transposed view, made contiguous on the device first)
 // with [lo, hi] = [-100, 100] for integer and [-300, 300] for floating-point dtypes.
+//   fused_<act>      ops::MulBiasAct(Random({2,64,96}, bf16, -1, 1, 90), Random({96,80}, bf16, -1, 1, 91),
+//                    &Random({80}, bf16, -2, 2, 92), act)          (B and the bias broadcast)
+//   fused_f32_full   ops::MulBiasAct(Random({64,96}, fp32, -1, 1, 93), Random({96,80}, fp32, -1, 1, 94),
+//                    &Random({64,80}, fp32, -2, 2, 95), Silu)
+//   "threw <name>" lines: calls that must throw (bias of the wrong dtype or shape).
 #include <cstdio>
 #include <fstream>
 #include <string>
@@ -68,6 +73,36 @@ int main(int argc, char** argv) {
                 return ops::Typecast(src.t(), dd);
             });
         }
+    for (int act = 0; act <= 4; ++act)
+        run("fused_" + std::to_string(act), [&] {
+            const Tensor bias = ops::Random({80}, DataType::BFLOAT16, -2.0f, 2.0f, 92);
+            return ops::MulBiasAct(ops::Random({2, 64, 96}, DataType::BFLOAT16, -1.0f, 1.0f, 90),
+                                   ops::Random({96, 80}, DataType::BFLOAT16, -1.0f, 1.0f, 91), &bias,
+                                   static_cast<ops::Activation>(act));
+        });
+    run("fused_f32_full", [&] {
+        const Tensor bias = ops::Random({64, 80}, DataType::FLOAT32, -2.0f, 2.0f, 95);
+        return ops::MulBiasAct(ops::Random({64, 96}, DataType::FLOAT32, -1.0f, 1.0f, 93),
+                               ops::Random({96, 80}, DataType::FLOAT32, -1.0f, 1.0f, 94), &bias, ops::Activation::Silu);
+    });
+    auto must_throw = [&](const std::string& name, auto&& f) {
+        try {
+            f();
+            std::printf("FAIL %s: no exception\n", name.c_str());
+            ++failures;
+        } catch (const std::exception& e) {
+            std::printf("threw %s: %s\n", name.c_str(), e.what());
+        }
+    };
+    const Tensor a = ops::Random({64, 96}, DataType::BFLOAT16, -1.0f, 1.0f, 1);
+    const Tensor b = ops::Random({96, 80}, DataType::BFLOAT16, -1.0f, 1.0f, 2);
+    const Tensor bias_f32 = ops::Random({80}, DataType::FLOAT32, -1.0f, 1.0f, 3);
+    const Tensor bias_short = ops::Random({40}, DataType::BFLOAT16, -1.0f, 1.0f, 4);
+    must_throw("bias_dtype", [&] { ops::MulBiasAct(a, b, &bias_f32, ops::Activation::Relu); });
+    must_throw("bias_shape", [&] { ops::MulBiasAct(a, b, &bias_short, ops::Activation::Relu); });
+    const Tensor ai = ops::Random({64, 96}, DataType::INT8, -3.0f, 3.0f, 5);
+    const Tensor bi = ops::Random({96, 80}, DataType::INT8, -3.0f, 3.0f, 6);
+    must_throw("int8_output", [&] { ops::MulBiasAct(ai, bi, nullptr, ops::Activation::Relu); });
     std::printf("failures %d\n", failures);
     return failures ? 1 : 0;
 }

@@ -40,7 +40,8 @@ def test_abi_version_matches_header():
     assert tv.lib().tv_hip_abi_version() == v
 
 
-@pytest.mark.parametrize("struct,cname", [("TvGemmArgs", "tv_gemm_args"), ("TvRepackArgs", "tv_repack_args")])
+@pytest.mark.parametrize("struct,cname", [("TvGemmArgs", "tv_gemm_args"), ("TvRepackArgs", "tv_repack_args"),
+                                         ("TvEpilogue", "tv_epilogue")])
 def test_struct_layout_matches_c(tmp_path, struct, cname):
     S = getattr(tv, struct)
     fields = [f for f, _ in S._fields_]
@@ -111,6 +112,29 @@ def test_elementwise_rejections():
     assert L.tv_hip_typecast(p, tv.INT8, p, tv.FLOAT32, 4, None) == tv.TV_E_INJECTED
     assert L.tv_hip_fill(p, tv.INT8, 4, 1.0, None) == tv.TV_E_INJECTED
     assert L.tv_hip_random(p, tv.INT8, 4, 0.0, 1.0, 1, None) == tv.TV_E_INJECTED
+    L.tv_hip_inject_fault(0, 0)
+
+
+def test_gemm_ex_rejections():
+    """The fused epilogue serves float outputs of the matrix-core pairs only."""
+    L = tv.lib()
+
+    def call(args, **ep):
+        e = tv.TvEpilogue()
+        for k, v in ep.items():
+            setattr(e, k, v)
+        return L.tv_hip_gemm_ex(ctypes.byref(args), ctypes.byref(e), None)
+
+    assert L.tv_hip_gemm_ex(None, None, None) == tv.TV_E_NULL
+    assert call(_args(), act=5) == tv.TV_E_UNSUPPORTED
+    assert call(_args(), act=-1) == tv.TV_E_UNSUPPORTED
+    assert call(_args(), act=tv.ACT_RELU, reserved=1) == tv.TV_E_UNSUPPORTED
+    assert call(_args(dtype_a=tv.INT8, dtype_b=tv.INT8, dtype_c=tv.INT8), act=tv.ACT_RELU) == tv.TV_E_UNSUPPORTED
+    assert call(_args(dtype_a=tv.INT32, dtype_b=tv.INT32, dtype_c=tv.INT32), act=tv.ACT_RELU) == tv.TV_E_UNSUPPORTED
+    assert call(_args(dtype_c=-1), act=tv.ACT_RELU) == tv.TV_E_DTYPE
+    assert call(_args(M=0, A=None, B=None, C=None), act=tv.ACT_SILU) == tv.TV_OK
+    L.tv_hip_inject_fault(tv.TV_E_INJECTED, 1)
+    assert call(_args(), act=tv.ACT_RELU) == tv.TV_E_INJECTED
     L.tv_hip_inject_fault(0, 0)
 
 

@@ -104,6 +104,40 @@ def test_cpp_typecast_of_transposed_view(init_run, s, d):
     np.testing.assert_array_equal(_read(out, name, d, (33, 257)), want)
 
 
+def _fused_ref(a, b, bias, act):
+    pre = np.matmul(a, b) + bias
+    return {0: pre, 1: np.maximum(pre, 0), 2: pre / (1 + np.exp(-pre)), 3: 1 / (1 + np.exp(-pre)), 4: np.tanh(pre)}[act]
+
+
+@pytest.mark.parametrize("act", range(5), ids=["none", "relu", "silu", "sigmoid", "tanh"])
+def test_cpp_mul_bias_act(init_run, act):
+    """ops::MulBiasAct: bf16 [2,64,96] @ broadcast [96,80] + per-column bias, then the activation,
+    within the bf16 bar (1e-2 relative plus the matmul bound) of the fp64 composition."""
+    r, out, done = init_run
+    assert f"fused_{act}" in done, r.stdout[-2000:]
+    a = to_value(rng.make("uniform", (2, 64, 96), 90, "bfloat16", -1, 1), BFLOAT16).astype(np.float64)
+    b = to_value(rng.make("uniform", (96, 80), 91, "bfloat16", -1, 1), BFLOAT16).astype(np.float64)
+    bias = to_value(rng.make("uniform", (80,), 92, "bfloat16", -2, 2), BFLOAT16).astype(np.float64)
+    ref = _fused_ref(a, b, bias, act)
+    got = to_value(_read(out, f"fused_{act}", BFLOAT16, (2, 64, 80)), BFLOAT16).astype(np.float64)
+    tol = 1e-2 * np.abs(ref) + 1e-5 * np.sqrt(96) * np.matmul(np.abs(a), np.abs(b)) + 1e-3
+    assert (np.abs(got - ref) <= tol).all()
+
+
+def test_cpp_mul_bias_act_fp32_full_bias_and_errors(init_run):
+    r, out, done = init_run
+    assert "fused_f32_full" in done, r.stdout[-2000:]
+    a = rng.make("uniform", (64, 96), 93, "float32", -1, 1).astype(np.float64)
+    b = rng.make("uniform", (96, 80), 94, "float32", -1, 1).astype(np.float64)
+    bias = rng.make("uniform", (64, 80), 95, "float32", -2, 2).astype(np.float64)
+    ref = _fused_ref(a, b, bias, 2)
+    got = _read(out, "fused_f32_full", FLOAT32, (64, 80)).astype(np.float64)
+    tol = 1e-5 * np.sqrt(96) * np.matmul(np.abs(a), np.abs(b)) + 1e-6 * np.abs(ref) + 1e-30
+    assert (np.abs(got - ref) <= tol).all()
+    for name in ("bias_dtype", "bias_shape", "int8_output"):
+        assert re.search(rf"^threw {name}: ", r.stdout, re.M), r.stdout[-2000:]
+
+
 def test_cpp_init_driver_exit_status(init_run):
     r, _, _ = init_run
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
