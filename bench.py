@@ -52,6 +52,10 @@ def make_inputs(name: str):
         q = rng.normal_f32(7, 32 * 2048 * 128) / np.float32(np.sqrt(128.0))
         k = rng.normal_f32(8, 32 * 2048 * 128) / np.float32(np.sqrt(128.0))
         return dict(a=rng.f32_to_f16_bits(q).reshape(32, 2048, 128), b=rng.f32_to_f16_bits(k).reshape(32, 2048, 128), dt=5)
+    if name == "c3_fused":
+        d = make_inputs("c3")
+        d["bias"] = rng.make("uniform", (4096,), 12, "bfloat16", lo=-1, hi=1)
+        return d
     if name in ("c5m1", "c5m8"):
         m = 1 if name == "c5m1" else 8
         return dict(a=rng.make("normal", (m, 4096), 9 if m == 1 else 11, "bfloat16"),
@@ -63,11 +67,12 @@ DESC = {
     "c1": "fp32 A[2592,2048] @ B[2048,4096] -> fp32 (README benchmark shape)",
     "c2": "int8 A[4096,4096] @ B[4096,4096] -> int8 (low byte of the int32 sum)",
     "c3": "bf16 A[16,2048,4096] @ B[4096,4096] (B broadcast over batch) -> bf16, fp32 accumulate",
+    "c3_fused": "c3 with the fused epilogue: silu(A @ B + bias[4096]) -> bf16 (tv_hip_gemm_ex)",
     "c4": "fp16 Q[32,2048,128] @ K.permute(0,2,1) (strided view, no repack) -> fp16 [32,2048,2048]",
     "c5m1": "bf16 GEMV x[1,4096] @ W[4096,11008] -> bf16, fp32 accumulate (6 W replicas rotated)",
     "c5m8": "bf16 GEMV x[8,4096] @ W[4096,11008] -> bf16, fp32 accumulate (6 W replicas rotated)",
 }
-DTYPE = {"c1": "fp32", "c2": "int8", "c3": "bf16", "c4": "fp16", "c5m1": "bf16", "c5m8": "bf16"}
+DTYPE = {"c1": "fp32", "c2": "int8", "c3": "bf16", "c3_fused": "bf16", "c4": "fp16", "c5m1": "bf16", "c5m8": "bf16"}
 
 
 def work(name: str, inp) -> tuple[float, float]:
@@ -113,9 +118,17 @@ def run_gpu(name: str, steps: int, warmup: int):
     descs = [tv.make_args(a, r, out) for r in reps]
     stream = torch.cuda.current_stream()
     sh = ctypes.c_void_p(stream.cuda_stream)
+    ep = None
+    if "bias" in inp:
+        bias = to_torch(inp["bias"], dt)
+        ep = tv.TvEpilogue()
+        ep.act, ep.bias, ep.sbias_b, ep.sbias_m, ep.sbias_n = tv.ACT_SILU, bias.data_ptr(), 0, 0, 1
 
     def step(i):
-        rc = L.tv_hip_gemm(ctypes.byref(descs[i % len(descs)]), sh)
+        if ep is None:
+            rc = L.tv_hip_gemm(ctypes.byref(descs[i % len(descs)]), sh)
+        else:
+            rc = L.tv_hip_gemm_ex(ctypes.byref(descs[i % len(descs)]), ctypes.byref(ep), sh)
         if rc:
             tv.check(rc)
 
@@ -170,6 +183,10 @@ def run_vendor(name: str, inp, steps: int, warmup: int) -> dict:
         bt = b.permute(0, 2, 1).contiguous()
         fn = lambda i: torch.bmm(a, bt)
         note = "torch.bmm with K^T materialised"
+    elif "bias" in inp:
+        bias = to_torch(inp["bias"], dt)
+        fn = lambda i: torch.nn.functional.silu(torch.matmul(a, b) + bias)  # noqa: E731
+        note = "torch.nn.functional.silu(torch.matmul(a, b) + bias) (three kernels)"
     else:
         reps = [b] + ([b.clone() for _ in range(5)] if name.startswith("c5") else [])
         fn = lambda i: torch.matmul(a, reps[i % len(reps)])
@@ -301,7 +318,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5m1,c5m8,cast_c3a,random_c3a,fill_c3a")
+    ap.add_argument("--configs", default="c1,c2,c3,c3_fused,c4,c5m1,c5m8,cast_c3a,random_c3a,fill_c3a")
     ap.add_argument("--only", default=None,
                     help="run only this config's GPU kernel (for profilers); 'copy' runs the traffic calibration copy")
     ap.add_argument("--no-cpu", action="store_true")
@@ -354,7 +371,7 @@ def main() -> int:
         log(f"cpu c2: {cpu['seconds']:.2f} s, {cpu['value'] * 1e3:.1f} GOP/s on {cpu['cores']} threads")
         if args.cpu_all:
             for n in names:
-                if n != "c2" and n not in EW:
+                if n != "c2" and n not in EW and n != "c3_fused":
                     log(f"cpu baseline {n}")
                     results[n]["cpu_baseline"] = run_cpu(n, inputs[n], iters=1)
 

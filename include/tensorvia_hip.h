@@ -107,7 +107,9 @@ enum tv_act {
 /* Fused epilogue: C[b, m, n] = act(sum_k A*B + bias[b, m, n]), computed on the fp32 accumulator and
  * rounded once to dtype_c.  Element (b, m, n) of the bias lives at bias + b*sbias_b + m*sbias_m +
  * n*sbias_n (element units, dtype = dtype_c); zero strides broadcast (sbias_b = sbias_m = 0,
- * sbias_n = 1 is a per-column bias vector).  bias = NULL adds nothing. */
+ * sbias_n = 1 is a per-column bias vector).  bias = NULL adds nothing.  Strides are non-negative
+ * and the bias elements read span at most 2^30 bytes (TV_E_SHAPE / TV_E_UNSUPPORTED otherwise).
+ * silu and sigmoid use the hardware's approximate exp2 and reciprocal (a few ulp in fp32). */
 typedef struct tv_epilogue {
     int32_t act;        /* enum tv_act */
     int32_t reserved;   /* must be 0 */
@@ -116,8 +118,8 @@ typedef struct tv_epilogue {
 } tv_epilogue;
 
 /* tv_hip_gemm with a fused epilogue (ep = NULL: same as tv_hip_gemm).  Served for the float-output
- * matrix-core pairs (fp32 -> fp32, bf16 -> bf16/fp32, fp16 -> fp16/fp32); integer outputs return
- * TV_E_UNSUPPORTED, an act outside enum tv_act TV_E_UNSUPPORTED. */
+ * matrix-core pairs (fp32 -> fp32, bf16 -> bf16/fp32, fp16 -> fp16/fp32); integer outputs and an
+ * act outside enum tv_act return TV_E_UNSUPPORTED. */
 int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_stream);
 
 /* Skinny-M (M <= 8) matrix-vector path: HBM-streaming, no matrix cores.  Returns

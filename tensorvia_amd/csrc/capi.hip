@@ -76,6 +76,7 @@ int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
     d->dtype_a = a->dtype_a; d->dtype_b = a->dtype_b; d->dtype_c = a->dtype_c;
     d->bias = nullptr;
     d->sbias_b = d->sbias_m = d->sbias_n = 0;
+    d->bias_bytes = 0;
     d->act = TV_ACT_NONE;
     (void)is_float_dt;
     return TV_OK;
@@ -124,10 +125,20 @@ int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_st
         if (ep->act < TV_ACT_NONE || ep->act > TV_ACT_TANH || ep->reserved != 0) return TV_E_UNSUPPORTED;
         const bool float_out = args->dtype_c == TV_FLOAT32 || args->dtype_c == TV_BFLOAT16 || args->dtype_c == TV_FLOAT16;
         if (!mfma_pair(args) || !float_out) return TV_E_UNSUPPORTED;
-        d.bias = ep->bias;
-        d.sbias_b = ep->sbias_b;
-        d.sbias_m = ep->sbias_m;
-        d.sbias_n = ep->sbias_n;
+        if (ep->bias) {
+            if (ep->sbias_b < 0 || ep->sbias_m < 0 || ep->sbias_n < 0) return TV_E_SHAPE;
+            // Extent of the elements read, in bytes: every offset stays below 2^30 (one buffer
+            // resource, 32-bit offsets).
+            const int64_t last = (d.batch - 1 > 0 ? (int64_t)(d.batch - 1) : 0) * ep->sbias_b +
+                                 (d.M > 0 ? d.M - 1 : 0) * ep->sbias_m + (d.N > 0 ? d.N - 1 : 0) * ep->sbias_n;
+            const int64_t bytes = (last + 1) * (int64_t)tvk::dtype_size(args->dtype_c);
+            if (last > ((int64_t)1 << 30) || bytes > ((int64_t)1 << 30)) return TV_E_UNSUPPORTED;
+            d.bias = ep->bias;
+            d.sbias_b = ep->sbias_b;
+            d.sbias_m = ep->sbias_m;
+            d.sbias_n = ep->sbias_n;
+            d.bias_bytes = bytes;
+        }
         d.act = ep->act;
     }
     return run_gemm(args, d, static_cast<hipStream_t>(hip_stream));

@@ -105,13 +105,26 @@ struct DmaOperand {
     // Loads k-tile k0 into `stage` (this wave's PER_WAVE blocks); ASM: through dma_load16_asm.
     template <bool ASM = false>
     __device__ inline void issue(char* stage, int wave, int k0) const {
-        __amdgpu_buffer_rsrc_t rs;
+        const char* p;
+        int64_t bytes;
         if constexpr (MODE == LOAD_KCONTIG) {
             const int rows = rows_valid < ROWS ? rows_valid : ROWS;
-            rs = make_rsrc(base + (int64_t)k0 * ES, (int64_t)rows * s_r * ES);
+            p = base + (int64_t)k0 * ES;
+            bytes = (int64_t)rows * s_r * ES;
         } else {
-            rs = make_rsrc(base + (int64_t)k0 * s_k * ES, (int64_t)(K - k0) * s_k * ES);
+            p = base + (int64_t)k0 * s_k * ES;
+            bytes = (int64_t)(K - k0) * s_k * ES;
         }
+        // The descriptor lives in scalar registers.  Its values are workgroup-uniform; reading them
+        // from the first lane states that to the compiler, which otherwise may treat them as
+        // per-lane values (the inline-assembly load then gets vector registers, the builtin a
+        // per-load loop over lanes).
+        const uint64_t u = reinterpret_cast<uint64_t>(p);
+        p = reinterpret_cast<const char*>(
+            (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)u) |
+            ((uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(u >> 32)) << 32));
+        const int nr = __builtin_amdgcn_readfirstlane(bytes <= 0 ? 0 : (bytes > 0x40000000 ? 0x40000000 : (int)bytes));
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p), (short)0, nr, 0x00020000);
 #pragma unroll
         for (int j = 0; j < PER_WAVE; ++j) {
             unsigned off = loff[j];
@@ -182,7 +195,7 @@ struct DmaOperand {
     static constexpr int kFragReads = MODE == LOAD_MNCONTIG ? 2 : 1;
 };
 
-template <class C>
+template <class C, bool FUSED = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
                           amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
 void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec) {
@@ -308,11 +321,18 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
     // load into LDS is left in flight when the workgroup ends); all waves leave the k-loop's LDS
     // before any wave stages its output there.
     wait_vmcnt<0>();
-    if constexpr (!__is_same(Acc, i32x4))
-        if (has_epilogue(d))
-            apply_epilogue<C>(acc, d, b, m0 + wm * C::WM + (lane & 15), n0 + wn * C::WN + (lane >> 4) * 4);
     const size_t csz = dtype_size(d.dtype_c);
     char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
+    if constexpr (FUSED && !__is_same(Acc, i32x4)) {
+        // Fused epilogue: fp32 staging, bias and activation after the accumulators are dead.
+        lds_barrier();
+        char* lw = (wave < NWAVES / 2 ? S0 : S1) + (wave % (NWAVES / 2)) * EPI;
+        const int mrow0 = m0 + wm * C::WM, ncol0 = n0 + wn * C::WN;
+        if (d.dtype_c == TV_BFLOAT16) write_tile_staged_epi<__bf16, C, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d, b, c_vec != 0);
+        else if (d.dtype_c == TV_FLOAT16) write_tile_staged_epi<_Float16, C, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d, b, c_vec != 0);
+        else write_tile_staged_epi<float, C, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d, b, c_vec != 0);
+        return;
+    }
     if (c_vec == 2) {
         lds_barrier();
         char* lw = (wave < NWAVES / 2 ? S0 : S1) + (wave % (NWAVES / 2)) * EPI;
@@ -491,10 +511,6 @@ void gemm_smallk_kernel(GemmDesc d, int tiles_m, int tiles_n) {
                     for (int j = 0; j < C::FN; ++j) Op::run(fb[j], fa[i], acc[i][j]);
             }
         }
-        // The fused epilogue reads its bias before the next tile's loads are issued.
-        if constexpr (!__is_same(Acc, i32x4))
-            if (has_epilogue(d))
-                apply_epilogue<C>(acc, d, b, m0 + wm * C::WM + (lane & 15), n0 + wn * C::WN + (lane >> 4) * 4);
         dma_barrier(); // every wave is done reading the operands
         const int cb = b, cm0 = m0, cn0 = n0;
         const int next = t + 1;
@@ -533,6 +549,15 @@ static int run_dma_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
     if (c_vec && d.sc_m % v16 == 0 && (d.batch <= 1 || d.sc_b % v16 == 0) &&
         (reinterpret_cast<uintptr_t>(d.C) % 16) == 0 && (C::WN * (int64_t)csz) % 16 == 0)
         c_vec = 2;
+    // The fused epilogue runs in the staged store only (16-byte aligned rows of C).
+    const bool epi = d.bias != nullptr || d.act != TV_ACT_NONE;
+    if (epi && d.sc_n != 1) return TV_E_UNSUPPORTED; // the fused store writes rows of C
+    if constexpr (!__is_same(typename C::T, int8_t))
+        if (epi) {
+            hipLaunchKernelGGL((gemm_dma_kernel<C, true>), dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
+                               group_m, c_vec);
+            return hipGetLastError();
+        }
     hipLaunchKernelGGL(gemm_dma_kernel<C>, dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
                        group_m, c_vec);
     return hipGetLastError();
@@ -572,7 +597,9 @@ static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m) {
     const int es = (int)sizeof(T);
     const int am = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, BM);
     const int bm = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, BN);
-    if (am != LOAD_GENERIC && bm != LOAD_GENERIC && smallk_ok(d, es, BM, BN)) {
+    // The small-K kernel has no fused epilogue (its staging area holds the output type only).
+    const bool epi = d.bias != nullptr || d.act != TV_ACT_NONE;
+    if (!epi && am != LOAD_GENERIC && bm != LOAD_GENERIC && smallk_ok(d, es, BM, BN)) {
 #define TV_CASE(A_, B_) \
     if (am == A_ && bm == B_) return run_smallk_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream);
         TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)

@@ -279,23 +279,6 @@ struct GemmCfg {
 // wrap), the reference CPU backend's int8 result; half outputs round to nearest even.
 template <typename TC, typename V> __device__ inline TC cvt_out(V v) { return static_cast<TC>(v); }
 
-// Fused epilogue on the wave's fp32 accumulators, in place: acc[i][j][q] is C[row0 + 16i][col0 + 16j
-// + q] of batch b.  Positions outside C keep their (unused) values.
-template <class C>
-__device__ inline void apply_epilogue(f32x4 (&acc)[C::FM][C::FN], const GemmDesc& d, int b, int row0, int col0) {
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i) {
-        const int row = row0 + 16 * i;
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int col = col0 + 16 * j + q;
-                if (row < d.M && col < d.N) acc[i][j][q] = epilogue_value(acc[i][j][q], d, b, row, col);
-            }
-    }
-}
-
 // Store the wave's accumulators as TC: acc[i][j][q] is C[row0 + 16i][col0 + 16j + q] (the lane's
 // row and first column are folded into row0 / col0), four consecutive columns per vector store.
 template <typename TC, class C, typename Acc>
@@ -392,6 +375,74 @@ __device__ inline void write_tile_staged(const Acc (&acc)[C::FM][C::FN], char* l
     }
 }
 
+// Staged store with the fused epilogue (float accumulators): the wave stages its fp32 accumulators
+// in its LDS area (rows padded by 16 bytes), then each lane takes 4 consecutive columns of a row,
+// adds their bias values, applies the activation and stores them rounded once to TC.  The
+// accumulators are dead before the bias is read, so the epilogue adds no register pressure to the
+// k-loop.  Requires row-contiguous C (sc_n == 1); vec_ok: rows aligned for 4-element stores.
+template <typename TC, class C, int WAVE_BYTES = kEpiWaveBytes>
+__device__ inline void write_tile_staged_epi(const f32x4 (&acc)[C::FM][C::FN], char* lds_wave, char* Cb, int lane,
+                                             int mrow0, int ncol0, const GemmDesc& d, int b, bool vec_ok) {
+    constexpr int ROWB = C::WN * 4;
+    constexpr int PITCH = ROWB + 16;
+    constexpr int RPP = staged_rows<C::WM, PITCH, WAVE_BYTES>();
+    constexpr int CPR = ROWB / 16; // 4-column float chunks per row
+    static_assert(RPP >= 16 && C::WM % RPP == 0 && RPP * PITCH <= WAVE_BYTES, "staging area too small");
+    typedef TC out4 __attribute__((__vector_size__(4 * sizeof(TC))));
+    const bool has_bias = d.bias != nullptr;
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(static_cast<const char*>(d.bias), has_bias ? d.bias_bytes : 0);
+    const int64_t base = (int64_t)b * d.sbias_b;
+    const bool logistic = d.act == TV_ACT_SILU || d.act == TV_ACT_SIGMOID || d.act == TV_ACT_TANH;
+    const ActCoef k = act_coef(d.act);
+#pragma unroll
+    for (int pass = 0; pass < C::WM / RPP; ++pass) {
+#pragma unroll
+        for (int i = pass * (RPP / 16); i < (pass + 1) * (RPP / 16); ++i) {
+            char* rowp = lds_wave + (16 * (i - pass * (RPP / 16)) + (lane & 15)) * PITCH + (lane >> 4) * 16;
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) *reinterpret_cast<f32x4*>(rowp + j * 64) = acc[i][j];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+        for (int idx = lane; idx < RPP * CPR; idx += 64) {
+            const int r = idx / CPR, c = idx % CPR;
+            const int row = mrow0 + pass * RPP + r;
+            const int col = ncol0 + c * 4;
+            f32x4 v = *reinterpret_cast<const f32x4*>(lds_wave + r * PITCH + c * 16);
+            if (has_bias) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const unsigned bi = row < d.M && col + q < d.N
+                                            ? (unsigned)(base + (int64_t)row * d.sbias_m + (int64_t)(col + q) * d.sbias_n)
+                                            : kOOB;
+                    v[q] += d.dtype_c == TV_FLOAT32 ? bias_load32(br, bi) : bias_load16(br, bi, d.dtype_c == TV_BFLOAT16);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = logistic ? act_logistic(v[q], k) : act_simple(v[q], d.act);
+            if (row >= d.M) continue;
+            TC* dst = reinterpret_cast<TC*>(Cb) + (int64_t)row * d.sc_m + col;
+            if (vec_ok && col + 4 <= d.N) {
+                out4 o;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) o[q] = cvt_out<TC>(v[q]);
+                *reinterpret_cast<out4*>(dst) = o;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (col + q < d.N) dst[q] = cvt_out<TC>(v[q]);
+            }
+        }
+        if (pass + 1 < C::WM / RPP) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        }
+    }
+}
+
 // Scheduling hints for the interleaved phases (LLVM AMDGPU sched_group_barrier masks).
 constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200, SG_VALU = 0x002;
 
@@ -405,7 +456,7 @@ __device__ inline void lds_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <class C>
+template <class C, bool FUSED = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
                           amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
 void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec) {
@@ -552,8 +603,16 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
     const int row0 = m0 + wm * C::WM + (lane & 15);
     const int col0 = n0 + wn * C::WN + (lane >> 4) * 4;
     const bool vec_ok = c_vec != 0;
-    if constexpr (!__is_same(Acc, i32x4))
-        if (has_epilogue(d)) apply_epilogue<C>(acc, d, b, row0, col0);
+    if constexpr (FUSED && !__is_same(Acc, i32x4)) {
+        // Fused epilogue: fp32 staging, bias and activation after the accumulators are dead.
+        lds_barrier();
+        char* lw = smem + wave * kEpiWaveBytes;
+        const int mrow0 = m0 + wm * C::WM, ncol0 = n0 + wn * C::WN;
+        if (d.dtype_c == TV_BFLOAT16) write_tile_staged_epi<__bf16, C>(acc, lw, Cb, lane, mrow0, ncol0, d, b, vec_ok);
+        else if (d.dtype_c == TV_FLOAT16) write_tile_staged_epi<_Float16, C>(acc, lw, Cb, lane, mrow0, ncol0, d, b, vec_ok);
+        else write_tile_staged_epi<float, C>(acc, lw, Cb, lane, mrow0, ncol0, d, b, vec_ok);
+        return;
+    }
     if (c_vec == 2) {
         // All waves are done with the k-loop's LDS stages before any wave reuses them.
         lds_barrier();
@@ -618,6 +677,15 @@ static int run_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
     if (c_vec && d.sc_m % v16 == 0 && (d.batch <= 1 || d.sc_b % v16 == 0) &&
         (reinterpret_cast<uintptr_t>(d.C) % 16) == 0 && (C::WN * (int64_t)csz) % 16 == 0)
         c_vec = 2;
+    // The fused epilogue runs in the staged store only (16-byte aligned rows of C).
+    const bool epi = d.bias != nullptr || d.act != TV_ACT_NONE;
+    if (epi && d.sc_n != 1) return TV_E_UNSUPPORTED; // the fused store writes rows of C
+    if constexpr (!__is_same(typename C::T, int8_t))
+        if (epi) {
+            hipLaunchKernelGGL((gemm_mfma_kernel<C, true>), dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
+                               group_m, c_vec);
+            return hipGetLastError();
+        }
     hipLaunchKernelGGL(gemm_mfma_kernel<C>, dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
                        group_m, c_vec);
     return hipGetLastError();

@@ -31,7 +31,8 @@ struct GemmDesc {
     // Fused epilogue (float outputs): C = act(acc + bias[b, m, n]) on the fp32 accumulator, rounded
     // once to dtype_c.  bias == nullptr: no bias; act == TV_ACT_NONE: identity.
     const void* bias;                  // element type dtype_c
-    int64_t sbias_b, sbias_m, sbias_n; // element strides (0 broadcasts)
+    int64_t sbias_b, sbias_m, sbias_n; // element strides (0 broadcasts), non-negative
+    int64_t bias_bytes;                // extent of the bias read (below 2^30)
     int32_t act;
 };
 
@@ -39,15 +40,29 @@ __device__ inline bool has_epilogue(const GemmDesc& d) { return d.bias != nullpt
 
 // The reference's activations on float values (src/backend/cpu/activate.cpp:8-40,
 // src/backend/cuda/activate.cu:8-36): relu x > 0 ? x : 0, silu x / (1 + exp(-x)),
-// sigmoid 1 / (1 + exp(-x)), tanh.
+// sigmoid 1 / (1 + exp(-x)), tanh(x).  The three logistic ones are one formula,
+// (a*x + c) * s + e with s = 1 / (1 + exp(-g*x)):
+//   silu    a = 1, c = 0, e = 0,  g = 1
+//   sigmoid a = 0, c = 1, e = 0,  g = 1
+//   tanh    a = 0, c = 2, e = -1, g = 2      (tanh x = 2 / (1 + exp(-2x)) - 1)
+// evaluated with the hardware's approximate exp2 and reciprocal (__expf, __fdividef): a few ulp
+// relative for silu / sigmoid, about 1e-7 absolute for tanh near 0.
+struct ActCoef {
+    float a, c, e, g;
+};
+__host__ __device__ inline ActCoef act_coef(int act) {
+    if (act == TV_ACT_SIGMOID) return ActCoef{0.0f, 1.0f, 0.0f, 1.0f};
+    if (act == TV_ACT_TANH) return ActCoef{0.0f, 2.0f, -1.0f, 2.0f};
+    return ActCoef{1.0f, 0.0f, 0.0f, 1.0f}; // silu
+}
+__device__ inline float act_logistic(float x, const ActCoef& k) {
+    const float s = __fdividef(1.0f, 1.0f + __expf(-k.g * x));
+    return (k.a * x + k.c) * s + k.e;
+}
+__device__ inline float act_simple(float x, int act) { return act == TV_ACT_RELU ? (x > 0.0f ? x : 0.0f) : x; }
 __device__ inline float act_apply(float x, int act) {
-    switch (act) {
-        case TV_ACT_RELU: return x > 0.0f ? x : 0.0f;
-        case TV_ACT_SILU: return x / (1.0f + expf(-x));
-        case TV_ACT_SIGMOID: return 1.0f / (1.0f + expf(-x));
-        case TV_ACT_TANH: return tanhf(x);
-        default: return x;
-    }
+    if (act == TV_ACT_SILU || act == TV_ACT_SIGMOID || act == TV_ACT_TANH) return act_logistic(x, act_coef(act));
+    return act_simple(x, act);
 }
 
 __device__ inline float bias_at(const GemmDesc& d, int64_t b, int64_t m, int64_t n) {
@@ -97,6 +112,16 @@ __device__ inline u32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, unsigned off) {
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const char* base, int64_t bytes) {
     const int nr = bytes <= 0 ? 0 : (bytes > 0x40000000 ? 0x40000000 : (int)bytes);
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, nr, 0x00020000);
+}
+
+// Bias element `idx` as float: fp32 storage, or 16-bit storage (bf16 when bf, else fp16); idx = kOOB
+// reads zero.
+__device__ inline float bias_load32(__amdgpu_buffer_rsrc_t r, unsigned idx) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)(idx == kOOB ? kOOB : idx * 4), 0, 0));
+}
+__device__ inline float bias_load16(__amdgpu_buffer_rsrc_t r, unsigned idx, bool bf) {
+    const unsigned short h = __builtin_amdgcn_raw_buffer_load_b16(r, (int)(idx == kOOB ? kOOB : idx * 2), 0, 0);
+    return bf ? (float)__builtin_bit_cast(__bf16, h) : (float)__builtin_bit_cast(_Float16, h);
 }
 
 __host__ __device__ inline size_t dtype_size(int dt) {
