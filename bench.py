@@ -227,7 +227,7 @@ def run_ew(name: str, steps: int, warmup: int) -> dict:
     n = 16 * 2048 * 4096
     sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     if name == "cast_c3a":
-        src = torch.empty(n, dtype=torch.uint8, device="cuda").view(torch.int16)  # bf16 storage
+        src = torch.empty(n, dtype=torch.int16, device="cuda")  # n bf16 elements (2-byte storage)
         tv.check(L.tv_hip_random(ctypes.c_void_p(src.data_ptr()), tv.BFLOAT16, n, -1.0, 1.0, 5, sh))
         dst = torch.empty(n, dtype=torch.float32, device="cuda")
         call = lambda: L.tv_hip_typecast(ctypes.c_void_p(src.data_ptr()), tv.BFLOAT16,  # noqa: E731
