@@ -30,10 +30,11 @@ struct GemmDesc {
     int32_t dtype_a, dtype_b, dtype_c;
     // Fused epilogue (float outputs): C = act(acc + bias[b, m, n]) on the fp32 accumulator, rounded
     // once to dtype_c.  bias == nullptr: no bias; act == TV_ACT_NONE: identity.
-    const void* bias;                  // element type dtype_c
-    int64_t sbias_b, sbias_m, sbias_n; // element strides (0 broadcasts), non-negative
-    int64_t bias_bytes;                // extent of the bias read (below 2^30)
-    int32_t act;
+    // Defaults: no epilogue, so a descriptor filled field by field without them is a plain matmul.
+    const void* bias = nullptr;                    // element type dtype_c
+    int64_t sbias_b = 0, sbias_m = 0, sbias_n = 0; // element strides (0 broadcasts), non-negative
+    int64_t bias_bytes = 0;                        // extent of the bias read (below 2^30)
+    int32_t act = TV_ACT_NONE;
 };
 
 __device__ inline bool has_epilogue(const GemmDesc& d) { return d.bias != nullptr || d.act != TV_ACT_NONE; }
