@@ -118,8 +118,9 @@ typedef struct tv_epilogue {
 } tv_epilogue;
 
 /* tv_hip_gemm with a fused epilogue (ep = NULL: same as tv_hip_gemm).  Served for the float-output
- * matrix-core pairs (fp32 -> fp32, bf16 -> bf16/fp32, fp16 -> fp16/fp32); integer outputs and an
- * act outside enum tv_act return TV_E_UNSUPPORTED. */
+ * matrix-core pairs (fp32 -> fp32, bf16 -> bf16/fp32, fp16 -> fp16/fp32) with row-contiguous C
+ * (sc_n = 1; any C layout when M <= 8); integer outputs, a column-strided C and an act outside
+ * enum tv_act return TV_E_UNSUPPORTED. */
 int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_stream);
 
 /* Skinny-M (M <= 8) matrix-vector path: HBM-streaming, no matrix cores.  Returns

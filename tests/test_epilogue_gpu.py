@@ -127,6 +127,28 @@ def test_gemv(M, act):
     run_case(tv.BFLOAT16, tv.BFLOAT16, 0, M, 2048, 1104, "col", act, seed=4 + M)
 
 
+@pytest.mark.parametrize("act", [tv.ACT_RELU, tv.ACT_TANH])
+def test_fp32_gemv(act):
+    """M <= 8 with fp32 inputs: the GEMV's fp32 path applies the epilogue per output value."""
+    run_case(tv.FLOAT32, tv.FLOAT32, 0, 4, 512, 300, "full", act, seed=12)
+
+
+def test_column_strided_output_is_rejected():
+    """The fused store writes rows of C: a column-strided C (sc_n != 1) on the GEMM path is refused
+    before any launch, and C is left untouched."""
+    import torch
+    a = storage_to_torch(rng.make("uniform", (64, 96), 13, "bfloat16"), tv.BFLOAT16)
+    b = storage_to_torch(rng.make("uniform", (96, 80), 14, "bfloat16"), tv.BFLOAT16)
+    ct = torch.zeros((80, 64), dtype=torch.bfloat16, device="cuda")
+    args = tv.make_args(a, b, ct.t())  # C[m, n] at m + 64 n
+    ep = tv.TvEpilogue()
+    ep.act = tv.ACT_RELU
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert tv.lib().tv_hip_gemm_ex(ctypes.byref(args), ctypes.byref(ep), s) == tv.TV_E_UNSUPPORTED
+    torch.cuda.synchronize()
+    assert not ct.any()
+
+
 def test_no_epilogue_equals_plain_gemm():
     """ep = NULL and act = NONE without bias are the plain matmul, bit for bit."""
     import torch
