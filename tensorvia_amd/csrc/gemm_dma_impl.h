@@ -15,15 +15,20 @@
 //                                pass reads over all 64 banks.
 //    Lanes past the matrix edge (rows, columns or k) get an out-of-range buffer offset; the load then
 //    writes zeros into LDS.
-//  * Two LDS stages, S0 and S1, are separate arrays and the k-loop is unrolled by two, so each LDS
-//    read names the stage it reads and the compiler waits only for loads into that stage.
-//  * B fragments are double-buffered in registers; each A fragment block is reloaded with the next
-//    k-group's right after its last MFMA.  One barrier per k-tile:
-//        read B of k-group 1 (tile t); MFMAs of k-group 0, reloading A blocks for k-group 1;
-//        MFMAs of k-group 1 on the first half of the A blocks;
+//  * Two LDS stages; a stage is one 128-byte k-tile of A and of B.  The main kernel lays LDS out as
+//    [A stage 0 | A stage 1 | B stage 0 | B stage 1] and addresses every fragment of a lane from
+//    one base address per operand (XOR for the swizzled bits, ds_read immediates for the stage,
+//    k-group and fragment offsets), so the loop holds few address registers.
+//  * Per k-tile and wave (two k-groups, 2 x FM x FN MFMAs), one workgroup barrier:
+//        region 1: rows of MFMAs on k-group 0; after row i, fragment A[i] is reloaded with
+//                  k-group 1, and the B fragments of k-group 1 are read;
 //        wait for tile t+1's loads; barrier (tile t+1 visible everywhere, stage of tile t free);
-//        load tile t+2 into the stage of tile t; read B and the first A blocks of tile t+1;
-//        MFMAs on the other half, reloading those A blocks for tile t+1.
+//        region 2: rows on k-group 1; the loads of tile t+2 into the freed stage go out one per
+//                  row; after row i, A[i] is reloaded with k-group 0 of tile t+1, and the B
+//                  fragments of tile t+1 are read.
+//    sched_group_barrier fixes the interleave (a row of MFMAs, then its reads).  The loads inside
+//    the loop are inline assembly that the compiler does not see as LDS writes, so it adds no
+//    waits of its own for them; every wait for them is an explicit vmcnt count.
 #pragma once
 #include "gemm_mfma_impl.h"
 
@@ -36,6 +41,12 @@ typedef __attribute__((address_space(3))) void lds_void;
 template <int N> __device__ inline void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// s_waitcnt on LDS / scalar-memory operations only.
+template <int N> __device__ inline void wait_lgkmcnt() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (N << 8));
 }
 
 // Workgroup barrier for the direct-load pipeline: this wave's LDS reads have completed (lgkmcnt)
@@ -54,6 +65,18 @@ __device__ inline void dma_load16_asm(__amdgpu_buffer_rsrc_t r, char* lds_dst, u
     const unsigned m0v = (unsigned)(uintptr_t)(lds_void*)lds_dst;
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(off), "s"(r)
                  : "memory", "m0");
+}
+
+// The same load for the main k-loop.  No memory clobber: the loop's LDS reads may be scheduled
+// around it (they read the other stage; the workgroup barriers order the stages).  FIRST: the
+// descriptor was just written by v_readfirstlane (5 wait states before a VMEM reads it); later
+// loads of the same k-tile need only the M0 wait state.
+template <bool FIRST>
+__device__ inline void dma_load16_loop(__amdgpu_buffer_rsrc_t r, unsigned m0v, unsigned off) {
+    if constexpr (FIRST)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(off), "s"(r) : "m0");
+    else
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(off), "s"(r) : "m0");
 }
 
 template <int MODE, int ROWS, int THREADS, int ES>
@@ -102,9 +125,24 @@ struct DmaOperand {
         }
     }
 
-    // Loads k-tile k0 into `stage` (this wave's PER_WAVE blocks); ASM: through dma_load16_asm.
-    template <bool ASM = false>
+    // Loads k-tile k0 into `stage` (this wave's PER_WAVE blocks).  Through inline assembly: the
+    // compiler then adds no waits of its own for the LDS it writes (callers wait with explicit
+    // vmcnt counts).
     __device__ inline void issue(char* stage, int wave, int k0) const {
+        const __amdgpu_buffer_rsrc_t rs = rsrc(k0);
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) {
+            unsigned off = loff[j];
+            if constexpr (MODE == LOAD_KCONTIG) off = k0 + kc[j] < K ? off : kOOB;
+            dma_load16_asm(rs, stage + (wave * PER_WAVE + j) * 1024, off);
+        }
+    }
+
+    // Buffer descriptor of k-tile k0.  It lives in scalar registers and its values are
+    // workgroup-uniform; reading them from the first lane states that to the compiler, which
+    // otherwise may treat them as per-lane values (the inline-assembly load would then get vector
+    // registers).
+    __device__ inline __amdgpu_buffer_rsrc_t rsrc(int k0) const {
         const char* p;
         int64_t bytes;
         if constexpr (MODE == LOAD_KCONTIG) {
@@ -115,24 +153,64 @@ struct DmaOperand {
             p = base + (int64_t)k0 * s_k * ES;
             bytes = (int64_t)(K - k0) * s_k * ES;
         }
-        // The descriptor lives in scalar registers.  Its values are workgroup-uniform; reading them
-        // from the first lane states that to the compiler, which otherwise may treat them as
-        // per-lane values (the inline-assembly load then gets vector registers, the builtin a
-        // per-load loop over lanes).
         const uint64_t u = reinterpret_cast<uint64_t>(p);
         p = reinterpret_cast<const char*>(
             (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)u) |
             ((uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(u >> 32)) << 32));
         const int nr = __builtin_amdgcn_readfirstlane(bytes <= 0 ? 0 : (bytes > 0x40000000 ? 0x40000000 : (int)bytes));
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p), (short)0, nr, 0x00020000);
-#pragma unroll
-        for (int j = 0; j < PER_WAVE; ++j) {
-            unsigned off = loff[j];
-            if constexpr (MODE == LOAD_KCONTIG) off = k0 + kc[j] < K ? off : kOOB;
-            if constexpr (ASM)
-                dma_load16_asm(rs, stage + (wave * PER_WAVE + j) * 1024, off);
-            else
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(stage + (wave * PER_WAVE + j) * 1024), 16, off, 0, 0, 0);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p), (short)0, nr, 0x00020000);
+    }
+    // Load j of this wave for k-tile k0 into the k-tile at LDS address `stage` (see issue()); j is
+    // a constant after unrolling, and load 0 is the first use of a fresh descriptor.
+    __device__ inline void issue_one(int j, __amdgpu_buffer_rsrc_t rs, unsigned stage, int wave, int k0) const {
+        unsigned off = loff[j];
+        if constexpr (MODE == LOAD_KCONTIG) off = k0 + kc[j] < K ? off : kOOB;
+        const unsigned m0v = stage + (unsigned)((wave * PER_WAVE + j) * 1024);
+        if (j == 0) dma_load16_loop<true>(rs, m0v, off);
+        else dma_load16_loop<false>(rs, m0v, off);
+    }
+
+    // Main-loop fragment addressing: one per-lane LDS address `xf` (fragment 0, k-group 0, first
+    // read, stage 0); every other fragment differs from it by an XOR that the lane's own bits do
+    // not use and an offset that fits a ds_read immediate:
+    //  K layout:   kc_off(w0 + 16f + lane%16, 4kg + lane/16) = (xf ^ 64kg) + 2048f  (the row
+    //              swizzle (row >> 1) & 7 does not depend on f; k-group 1 flips chunk bit 2);
+    //  M/N layout: chunk (q0 + step f) ^ swz(kr) = (q0 ^ swz(kr)) ^ (step f) because q0 has no bits
+    //              below the fragment count times `step`; swz is the same for both reads of a lane
+    //              (k rows kr and kr + 8 / kr + 4) and both k-groups (kr + 64 / kr + 32), so
+    //              address = (xf ^ (f << FSH)) + 16384 kg + 2048 (second read).
+    unsigned xf;
+    static constexpr int FSH = ES == 1 ? 4 : 5;
+    __device__ inline void xinit(unsigned op_base, int lane, int w0) {
+        const int fr = lane & 15, grp = lane >> 4;
+        if constexpr (MODE == LOAD_KCONTIG) {
+            xf = op_base + kc_off(w0 + fr, grp);
+        } else if constexpr (ES == 1) {
+            const int kr = grp * 16 + (fr >> 1);
+            xf = op_base + kr * RB + (fr & 1) * 8 + (((w0 / 16) ^ swz(kr)) << 4);
+        } else {
+            const int kr = grp * 8 + (fr >> 2);
+            const int c = fr & 3;
+            xf = op_base + kr * RB + (c >> 1) * 16 + (c & 1) * 8 + (((w0 / 8) ^ swz(kr)) << 4);
+        }
+    }
+    // Fragment f of k-group kg in stage `st` (stage stride BYTES).
+    __device__ inline u32x4 frag_at(int st, int kg, int f) const {
+        if constexpr (MODE == LOAD_KCONTIG) {
+            const lds_char* p = (const lds_char*)(uintptr_t)(xf ^ (unsigned)(kg << 6)) + st * BYTES + f * 2048;
+            return *(const __attribute__((address_space(3))) u32x4*)p;
+        } else {
+            const lds_char* p = (const lds_char*)(uintptr_t)(xf ^ (unsigned)(f << FSH)) + st * BYTES + kg * 16384;
+            if constexpr (ES == 1) {
+                const i32x2_t a = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
+                const i32x2_t b = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(p + 2048));
+                return u32x4{(unsigned)a.x, (unsigned)a.y, (unsigned)b.x, (unsigned)b.y};
+            } else {
+                const i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
+                const i16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 2048));
+                const uint2 l2 = __builtin_bit_cast(uint2, a), h2 = __builtin_bit_cast(uint2, b);
+                return u32x4{l2.x, l2.y, h2.x, h2.y};
+            }
         }
     }
 
@@ -210,8 +288,15 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
     static_assert(NWAVES % 2 == 0, "the epilogue gives half of the waves to each stage array");
     constexpr int EPI = STAGE / (NWAVES / 2) / 16 * 16; // staging bytes per wave in the epilogue
 
-    __shared__ __attribute__((aligned(1024))) char S0[STAGE];
-    __shared__ __attribute__((aligned(1024))) char S1[STAGE];
+    // LDS: [A stage 0 | A stage 1 | B stage 0 | B stage 1]; the epilogue reuses all of it.
+    __shared__ __attribute__((aligned(1024))) char L[2 * STAGE];
+    char* const S0 = L;
+    char* const S1 = L + STAGE;
+    const unsigned LA0 = (unsigned)(uintptr_t)(lds_void*)L;
+    const unsigned LB0 = LA0 + 2 * LA::BYTES;
+    static_assert(LA::BYTES + 16384 + 2048 < 65536 && LB::BYTES + 16384 + 2048 < 65536 &&
+                      LA::BYTES + (C::FM - 1) * 2048 < 65536 && LB::BYTES + (C::FN - 1) * 2048 < 65536,
+                  "stage 1 and fragment offsets must fit a ds_read immediate");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -242,8 +327,8 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
     lb.s_r = d.sb_n; lb.s_k = d.sb_k; lb.rows_valid = d.N - n0; lb.K = d.K;
     la.init(wave, lane);
     lb.init(wave, lane);
-    la.frag_init(lane, wm * C::WM);
-    lb.frag_init(lane, wn * C::WN);
+    la.xinit(LA0, lane, wm * C::WM);
+    lb.xinit(LB0, lane, wn * C::WN);
 
     Acc acc[C::FM][C::FN];
 #pragma unroll
@@ -251,70 +336,88 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
 
-    // A fragments: one set, each block reloaded with the next k-group's right after its last MFMA.
-    // B fragments: double-buffered (every A block of a k-group uses all of them).
+    // A fragments: one set, each reloaded with the next k-group's right after its row of MFMAs.
+    // B fragments: one set per k-group of the k-tile (every row of a k-group uses all of them).
     u32x4 fa[C::FM], fb0[C::FN], fb1[C::FN];
-    auto read_b = [&](const char* stage, int kg, u32x4 (&fb)[C::FN]) {
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j) fb[j] = lb.frag(stage + LA::BYTES, kg, j);
-    };
     auto row = [&](int i, const u32x4 (&fb)[C::FN]) {
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) Op::run(fb[j], fa[i], acc[i][j]); // B fragment first: lanes hold 4 columns
     };
-    auto load_tile = [&](char* stage, int kt) {
-        la.issue(stage, wave, kt * C::BK);
-        lb.issue(stage + LA::BYTES, wave, kt * C::BK);
-    };
-    constexpr int H = C::FM / 2;
+    constexpr int NA = LA::PER_WAVE, NB = LB::PER_WAVE, NDMA = NA + NB;
+    static_assert(NDMA <= C::FM, "one load per row of MFMAs");
+    // Reads after each row: the row's A reload, plus B fragment i after rows i < FN.
+    static_assert(C::FN <= C::FM, "one B fragment per row");
+    constexpr int RD_B = 1 + LB::kFragReads;
 
-    // One k-tile in stage `sc`; tile kt+1 is being loaded into `sn`.  On entry fa / fb0 hold k-group
-    // 0 of tile kt.
-    auto step = [&](char* sc, char* sn, int kt, int nk) {
-        read_b(sc, 1, fb1);
+    // Interleave of a region: each row's FN MFMAs, then the reads that follow that row.
+    auto sched_rows = [] {
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, C::FN, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, RD_B, 0);
+        }
+#pragma unroll
+        for (int i = C::FN; i < C::FM; ++i) {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, C::FN, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // One k-tile: stage `cs` holds tile kt (k-group 0 already in fa / fb0); stage 1 - cs holds
+    // tile kt + 1 once the barrier has passed.
+    //   Region 1: rows on k-group 0; after row i reload fa[i] with k-group 1 and read fb1[i].
+    //   Wait for tile kt+1's loads, barrier (tile kt+1 visible, stage cs free).
+    //   Region 2: rows on k-group 1; one load of tile kt+2 into stage cs per row; after row i
+    //   reload fa[i] with k-group 0 of tile kt+1 and read its fb0[i].
+    auto step = [&](int cs, int kt) {
+        const int ns = 1 - cs;
 #pragma unroll
         for (int i = 0; i < C::FM; ++i) {
             row(i, fb0);
-            fa[i] = la.frag(sc, 1, i);
+            fa[i] = la.frag_at(cs, 1, i);
+            if (i < C::FN) fb1[i] = lb.frag_at(cs, 1, i);
         }
-#pragma unroll
-        for (int i = 0; i < H; ++i) row(i, fb1);
-        __builtin_amdgcn_sched_barrier(0);
-        // Tile kt+1 (the only loads in flight) has landed in this wave's blocks; after the barrier
-        // it has landed everywhere and every wave is done reading `sc`.
+        sched_rows();
+        const int k2 = (kt + 2) * C::BK;
+        const __amdgpu_buffer_rsrc_t ra = la.rsrc(k2);
+        const __amdgpu_buffer_rsrc_t rb = lb.rsrc(k2);
         wait_vmcnt<0>();
-        lds_barrier();
-        // Unconditional: past the last tile every lane is out of range and the loads write zeros
-        // into `sc`, which is not read again.  (A branch here would also make the compiler wait for
-        // all loads before any LDS read after the join.)
-        load_tile(sc, kt + 2);
-        read_b(sn, 0, fb0);
+        dma_barrier();
+        const unsigned sa = LA0 + (unsigned)(cs * LA::BYTES), sb = LB0 + (unsigned)(cs * LB::BYTES);
 #pragma unroll
-        for (int i = 0; i < H; ++i) fa[i] = la.frag(sn, 0, i);
-#pragma unroll
-        for (int i = H; i < C::FM; ++i) {
+        for (int i = 0; i < C::FM; ++i) {
             row(i, fb1);
-            fa[i] = la.frag(sn, 0, i);
+            if (i < NA) la.issue_one(i, ra, sa, wave, k2);
+            else if (i < NDMA) lb.issue_one(i - NA, rb, sb, wave, k2);
+            if (i < C::FN) fb0[i] = lb.frag_at(ns, 0, i);
+            fa[i] = la.frag_at(ns, 0, i);
         }
-        __builtin_amdgcn_sched_barrier(0);
+        sched_rows();
+        // Row 0 of the next step needs fb0 and fa[0]: only the A reloads after the last B read
+        // may still be in flight.
+        wait_lgkmcnt<C::FM - C::FN + 1>();
     };
 
     const int nk = (d.K + C::BK - 1) / C::BK;
-    // Prologue: tiles 0 and 1 in flight, then F0 of tile 0.
-    load_tile(S0, 0);
-    load_tile(S1, 1); // all out of range (zeros) when nk == 1
-    constexpr int NDMA = LA::PER_WAVE + LB::PER_WAVE; // loads per k-tile and wave
+    // Prologue: tiles 0 and 1 in flight, then k-group 0 of tile 0.
+    la.issue(S0, wave, 0);
+    lb.issue(L + 2 * LA::BYTES, wave, 0);
+    la.issue(L + LA::BYTES, wave, C::BK); // all out of range (zeros) when nk == 1
+    lb.issue(L + 2 * LA::BYTES + LB::BYTES, wave, C::BK);
     wait_vmcnt<NDMA>();
     lds_barrier();
-    read_b(S0, 0, fb0);
 #pragma unroll
-    for (int i = 0; i < C::FM; ++i) fa[i] = la.frag(S0, 0, i);
+    for (int j = 0; j < C::FN; ++j) fb0[j] = lb.frag_at(0, 0, j);
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) fa[i] = la.frag_at(0, 0, i);
+    wait_lgkmcnt<C::FM - 1>();
 
     // The step count is rounded up to even: a step past K multiplies the zeros loaded there, and
     // the loop has no conditional tail (the accumulators stay in place across the loop).
     for (int kt = 0; kt < nk; kt += 2) {
-        step(S0, S1, kt, nk);
-        step(S1, S0, kt + 1, nk);
+        step(0, kt);
+        step(1, kt + 1);
     }
 
     // Epilogue.  The zero-filling loads issued by the last steps land before anything else (no
@@ -470,16 +573,16 @@ void gemm_smallk_kernel(GemmDesc d, int tiles_m, int tiles_n) {
         lb.base = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)n0 * d.sb_n) * ES;
         lb.rows_valid = live ? d.N - n0 : 0;
         lb.init(wave, lane);
-        lb.template issue<true>(SB, wave, 0);
-        lb.template issue<true>(SB + LB::BYTES, wave, C::BK); // zeros when K fits in one k-tile
+        lb.issue(SB, wave, 0);
+        lb.issue(SB + LB::BYTES, wave, C::BK); // zeros when K fits in one k-tile
         if (live && (b != cur_b || m0 != cur_m0)) { // uniform over the workgroup
             cur_b = b;
             cur_m0 = m0;
             la.base = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + (int64_t)m0 * d.sa_m) * ES;
             la.rows_valid = d.M - m0;
             la.init(wave, lane);
-            la.template issue<true>(SA, wave, 0);
-            la.template issue<true>(SA + LA::BYTES, wave, C::BK);
+            la.issue(SA, wave, 0);
+            la.issue(SA + LA::BYTES, wave, C::BK);
         }
     };
 
