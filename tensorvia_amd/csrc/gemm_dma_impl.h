@@ -474,9 +474,10 @@ constexpr int kSmallKEpiBytes = 2304; // per wave: 16 rows of a 64-column 16-bit
 // Staged store for the small-K kernel: as write_tile_staged, but every wave issues the same number
 // of 16-byte buffer stores (chunks outside the matrix get an out-of-range offset and are dropped),
 // so a later vmcnt wait can count them.  Requires N and the row pitch in whole 16-byte chunks.
-// The stores are nontemporal (nt): the output is written once and never re-read by this launch,
-// and streaming it past the caches keeps them for the next tile's B and the resident A
-// (c4 fp16: 99.7 -> 73.1 us).
+// The stores are nontemporal (cache-policy bit nt = 2), and also sc1 (16) when a wave row is whole
+// 128-byte lines: the output is written once and never re-read by this launch, and streaming it
+// past the caches keeps them for the next tile's B and the resident A (c4 fp16: plain 99.7 us,
+// nt 73.1 us, nt sc1 68-69 us).
 template <typename TC, class C, typename Acc, int WAVE_BYTES>
 __device__ inline void write_tile_fixed(const Acc (&acc)[C::FM][C::FN], char* lds_wave, __amdgpu_buffer_rsrc_t cr,
                                         int lane, int mrow0, int ncol0, const GemmDesc& d) {
@@ -511,7 +512,7 @@ __device__ inline void write_tile_fixed(const Acc (&acc)[C::FM][C::FN], char* ld
             const int col = ncol0 + c * (16 / (int)sizeof(TC));
             const u32x4 v = *reinterpret_cast<const u32x4*>(lds_wave + r * PITCH + c * 16);
             const unsigned off = row < d.M && col < d.N ? (unsigned)(((int64_t)row * d.sc_m + col) * (int64_t)sizeof(TC)) : kOOB;
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), cr, (int)off, 0, 2);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), cr, (int)off, 0, ROWB % 128 == 0 ? 18 : 2);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
         __builtin_amdgcn_wave_barrier();

@@ -359,7 +359,8 @@ __device__ inline void write_tile_staged(const Acc (&acc)[C::FM][C::FN], char* l
             const u32x4 v = *reinterpret_cast<const u32x4*>(lds_wave + r * PITCH + c * 16);
             TC* dst = reinterpret_cast<TC*>(Cb) + (int64_t)row * d.sc_m + col;
             if (col + 16 / (int)sizeof(TC) <= d.N) {
-                *reinterpret_cast<u32x4*>(dst) = v;
+                if constexpr (ROWB % 128 == 0) store_stream16(dst, v); // whole lines per row
+                else *reinterpret_cast<u32x4*>(dst) = v;
             } else {
                 const TC* e = reinterpret_cast<const TC*>(&v);
 #pragma unroll
@@ -428,7 +429,9 @@ __device__ inline void write_tile_staged_epi(const f32x4 (&acc)[C::FM][C::FN], c
                 out4 o;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) o[q] = cvt_out<TC>(v[q]);
-                *reinterpret_cast<out4*>(dst) = o;
+                if constexpr (C::WN * sizeof(TC) % 128 != 0) *reinterpret_cast<out4*>(dst) = o; // part lines
+                else if constexpr (sizeof(out4) == 16) store_stream16(dst, __builtin_bit_cast(u32x4, o));
+                else store_stream8(dst, __builtin_bit_cast(uint2, o));
             } else {
 #pragma unroll
                 for (int q = 0; q < 4; ++q)

@@ -17,6 +17,17 @@ typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
 typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
 
+// Global stores with the streaming write policy (nt sc1) for output tiles that are written once.
+// Used only where every wave instruction writes whole 128-byte lines (rows of a staged tile): there
+// the policy saves the L2 the output's lines (c3 bf16 epilogue -3 %, c4 -6 %); on stores that
+// cover half lines per instruction it is several times slower than a plain store.
+__device__ inline void store_stream16(void* p, u32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1 nt" ::"v"(p), "v"(v) : "memory");
+}
+__device__ inline void store_stream8(void* p, uint2 v) {
+    asm volatile("global_store_dwordx2 %0, %1, off sc1 nt" ::"v"(p), "v"(v) : "memory");
+}
+
 // Descriptor the launchers receive: tv_gemm_args after validation, with sizes narrowed to the
 // ranges the kernels index with.
 struct GemmDesc {
