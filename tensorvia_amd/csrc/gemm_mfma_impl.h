@@ -395,6 +395,20 @@ __device__ inline void write_tile_staged_epi(const f32x4 (&acc)[C::FM][C::FN], c
     const int64_t base = (int64_t)b * d.sbias_b;
     const bool logistic = d.act == TV_ACT_SILU || d.act == TV_ACT_SIGMOID || d.act == TV_ACT_TANH;
     const ActCoef k = act_coef(d.act);
+    auto bias_elem = [&](int row, int col) {
+        const unsigned bi = row < d.M && col < d.N ? (unsigned)(base + (int64_t)row * d.sbias_m + (int64_t)col * d.sbias_n)
+                                                   : kOOB;
+        return d.dtype_c == TV_FLOAT32 ? bias_load32(br, bi) : bias_load16(br, bi, d.dtype_c == TV_BFLOAT16);
+    };
+    // A bias with no row stride (one value per column, as a per-channel bias): every chunk a lane
+    // writes has the same 4 columns (64 lanes cover whole rows of chunks), so the lane loads its 4
+    // values once instead of once per row.
+    static_assert(64 % CPR == 0, "a lane's chunk column is the same in every pass");
+    const bool col_bias = has_bias && d.sbias_m == 0;
+    float cbias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (col_bias)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cbias[q] = bias_elem(0, ncol0 + (lane % CPR) * 4 + q);
 #pragma unroll
     for (int pass = 0; pass < C::WM / RPP; ++pass) {
 #pragma unroll
@@ -412,14 +426,12 @@ __device__ inline void write_tile_staged_epi(const f32x4 (&acc)[C::FM][C::FN], c
             const int row = mrow0 + pass * RPP + r;
             const int col = ncol0 + c * 4;
             f32x4 v = *reinterpret_cast<const f32x4*>(lds_wave + r * PITCH + c * 16);
-            if (has_bias) {
+            if (col_bias) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const unsigned bi = row < d.M && col + q < d.N
-                                            ? (unsigned)(base + (int64_t)row * d.sbias_m + (int64_t)(col + q) * d.sbias_n)
-                                            : kOOB;
-                    v[q] += d.dtype_c == TV_FLOAT32 ? bias_load32(br, bi) : bias_load16(br, bi, d.dtype_c == TV_BFLOAT16);
-                }
+                for (int q = 0; q < 4; ++q) v[q] += cbias[q];
+            } else if (has_bias) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] += bias_elem(row, col + q);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] = logistic ? act_logistic(v[q], k) : act_simple(v[q], d.act);
