@@ -382,9 +382,10 @@ static int gemv_nl(const GemmDesc& d) {
     return nch >= 8 ? 8 : (nch >= 4 ? 4 : 2);
 }
 
-// K slices: enough for about 1376 workgroups in all at M <= 2 and 344 above (W[4096, 11008] bf16:
-// 172 strips x 8 or x 2, measured best; larger M has a longer per-workgroup reduction), at least what
-// x's LDS slice needs, and no more than leaves every k-lane two row groups per slice.
+// K slices: enough for about 1376 workgroups in all at M <= 2, 688 at M <= 4 and 344 above
+// (W[4096, 11008] bf16: 172 strips x 8, x 4 or x 2, measured best; larger M has a longer
+// per-workgroup reduction), at least what x's LDS slice needs, and no more than leaves every
+// k-lane two row groups per slice.
 static GemvPlan gemv_plan(const GemmDesc& d) {
     const int nl = gemv_nl(d);
     const int vec = 16 / (int)dtype_size(d.dtype_a);
@@ -393,7 +394,7 @@ static GemvPlan gemv_plan(const GemmDesc& d) {
     const int min_s = (d.K + kcap - 1) / kcap;
     const int rows_min = 2 * kGemvGroupRows * (kGemvThreads / nl);
     const int max_s = d.K / rows_min > 1 ? d.K / rows_min : 1;
-    const int64_t target = d.M <= 2 ? 1376 : 344;
+    const int64_t target = d.M <= 2 ? 1376 : (d.M <= 4 ? 688 : 344);
     int s = (int)((target + strips - 1) / strips);
     if (s > max_s) s = max_s;
     if (s > kGemvMaxSlices) s = kGemvMaxSlices;
