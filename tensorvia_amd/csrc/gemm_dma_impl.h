@@ -58,9 +58,10 @@ __device__ inline void dma_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// The same direct load, hidden from the compiler: it then adds no waits of its own for the LDS it
-// writes (callers wait with explicit vmcnt counts).  M0 is written right before the load; the
-// s_nop covers the M0 and descriptor-register read-after-write wait states.
+// The direct load (buffer_load_dwordx4 ... lds: 16 bytes per lane into LDS at M0 + 16 * lane) in
+// inline assembly, hidden from the compiler: it then adds no waits of its own for the LDS it writes
+// (callers wait with explicit vmcnt counts).  M0 is written right before the load; the s_nop covers
+// the M0 and descriptor-register read-after-write wait states.
 __device__ inline void dma_load16_asm(__amdgpu_buffer_rsrc_t r, char* lds_dst, unsigned off) {
     const unsigned m0v = (unsigned)(uintptr_t)(lds_void*)lds_dst;
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(off), "s"(r)
