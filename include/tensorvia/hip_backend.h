@@ -6,6 +6,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <memory>
+#include <mutex>
 
 #include "context.h"
 #include "ops.h"
@@ -16,6 +17,11 @@
 class HIPContext : public ContextImpl {
     int m_device_id = 0;
     hipStream_t m_stream = nullptr;
+    // Pinned staging for copies of pageable host memory (allocated on first use).
+    struct Staging;
+    std::unique_ptr<Staging> m_staging;
+    std::mutex m_staging_mu;
+    Staging& staging();
 
 public:
     HIPContext();
@@ -24,6 +30,11 @@ public:
     hipStream_t stream() const { return m_stream; }
     int device_id() const { return m_device_id; }
     void wait() const;
+    // Copies between pageable host memory and device memory on the context stream; they return
+    // once the copy has completed.  Large copies go through two pinned chunks, the host-side
+    // memcpy of one chunk overlapping the DMA of the other; small ones are direct.
+    void copy_h2d(void* dst, const void* src, size_t bytes);
+    void copy_d2h(void* dst, const void* src, size_t bytes);
     // The process-wide context, created on first use (no GPU is touched at library load).
     static std::shared_ptr<HIPContext> get();
 };

@@ -32,7 +32,7 @@ def build(verbose: bool = False) -> Path:
         list(ex.map(lambda c: be._run(c, verbose), jobs))
     tmp = be.HOST_LIB.with_suffix(".so.tmp")
     be._run([CXX, "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-             f"-L{be.PKG}", "-ltv_hip", f"-L{ROCM}/lib", "-lamdhip64",
+             f"-L{be.PKG}", "-ltv_hip", f"-L{ROCM}/lib", "-lamdhip64", "-pthread",
              "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM}/lib"], verbose)
     os.replace(tmp, be.HOST_LIB)
     return be.HOST_LIB

@@ -2,9 +2,13 @@
 // Mirrors the reference CUDA backend's roles (include/backend/cuda/cuda_context.h:8-68,
 // cuda_tensor.cpp:14-70, cuda_copy.cpp:9-26, src/init.cpp:18-34, src/backend/cuda/mul.cu:52-124)
 // on the C-ABI of include/tensorvia_hip.h.
+#include <algorithm>
+#include <condition_variable>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
+#include <vector>
 
 #include "tensorvia/factory.h"
 #include "tensorvia/hip_backend.h"
@@ -47,11 +51,156 @@ HIPContext::HIPContext() {
     hip_check(hipStreamCreate(&m_stream), "hipStreamCreate");
 }
 
+// Two pinned chunks, the events that mark the DMA last issued from each, and the host threads that
+// split each chunk's memcpy (one thread copies a pageable buffer at about half the rate the DMA
+// engines move a pinned one).
+struct HIPContext::Staging {
+    static constexpr size_t kChunk = size_t(16) << 20;
+    void* buf[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+
+    int nthreads = 1;
+    std::vector<std::thread> workers;
+    std::mutex mu;
+    std::condition_variable go, fin;
+    char* job_dst = nullptr;
+    const char* job_src = nullptr;
+    size_t job_len = 0, job_part = 0;
+    unsigned gen = 0;
+    int left = 0;
+    bool stop = false;
+
+    Staging() {
+        const unsigned hw = std::thread::hardware_concurrency();
+        nthreads = static_cast<int>(std::min(8u, hw ? hw : 1u));
+        for (int i = 1; i < nthreads; ++i) workers.emplace_back([this, i] { work(i); });
+    }
+    ~Staging() {
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            stop = true;
+        }
+        go.notify_all();
+        for (auto& t : workers) t.join();
+        for (int i = 0; i < 2; ++i) {
+            if (done[i]) (void)hipEventDestroy(done[i]);
+            if (buf[i]) (void)hipHostFree(buf[i]);
+        }
+    }
+    // Part i of the current job: [i * job_part, (i + 1) * job_part) clipped to job_len.
+    void copy_part(int i) const {
+        const size_t b = std::min(job_len, i * job_part), e = std::min(job_len, (i + 1) * job_part);
+        if (e > b) std::memcpy(job_dst + b, job_src + b, e - b);
+    }
+    void work(int i) {
+        unsigned seen = 0;
+        std::unique_lock<std::mutex> lk(mu);
+        for (;;) {
+            go.wait(lk, [&] { return stop || gen != seen; });
+            if (stop) return;
+            seen = gen;
+            lk.unlock();
+            copy_part(i);
+            lk.lock();
+            if (--left == 0) fin.notify_one();
+        }
+    }
+    // memcpy split over the threads in page-aligned parts; returns when every part is done.
+    void copy(void* dst, const void* src, size_t n) {
+        if (nthreads == 1 || n < (size_t(1) << 20)) {
+            std::memcpy(dst, src, n);
+            return;
+        }
+        std::unique_lock<std::mutex> lk(mu);
+        job_dst = static_cast<char*>(dst);
+        job_src = static_cast<const char*>(src);
+        job_len = n;
+        job_part = (n / nthreads + 4095) & ~size_t(4095);
+        left = nthreads - 1;
+        ++gen;
+        lk.unlock();
+        go.notify_all();
+        copy_part(0);
+        lk.lock();
+        fin.wait(lk, [&] { return left == 0; });
+    }
+};
+
+// Copies below this size go straight through hipMemcpyAsync.
+static constexpr size_t kStagingMin = size_t(4) << 20;
+
 HIPContext::~HIPContext() {
+    if (m_stream) (void)hipStreamSynchronize(m_stream);
+    m_staging.reset();
     if (m_stream) (void)hipStreamDestroy(m_stream);
 }
 
 void HIPContext::wait() const { hip_check(hipStreamSynchronize(m_stream), "hipStreamSynchronize"); }
+
+HIPContext::Staging& HIPContext::staging() {
+    if (!m_staging) {
+        auto st = std::make_unique<Staging>();
+        for (int i = 0; i < 2; ++i) {
+            hip_check(hipHostMalloc(&st->buf[i], Staging::kChunk, hipHostMallocDefault), "hipHostMalloc (staging)");
+            hip_check(hipEventCreateWithFlags(&st->done[i], hipEventDisableTiming), "hipEventCreate (staging)");
+        }
+        m_staging = std::move(st);
+    }
+    return *m_staging;
+}
+
+void HIPContext::copy_h2d(void* dst, const void* src, size_t bytes) {
+    if (bytes < kStagingMin) {
+        hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, m_stream), "hipMemcpyAsync H2D");
+        wait();
+        return;
+    }
+    std::lock_guard<std::mutex> lk(m_staging_mu);
+    Staging& st = staging();
+    size_t i = 0;
+    for (size_t off = 0; off < bytes; off += Staging::kChunk, ++i) {
+        const size_t n = std::min(Staging::kChunk, bytes - off);
+        const int b = static_cast<int>(i & 1);
+        // The DMA that last read this chunk (two chunks ago) has finished; then refill it while
+        // the other chunk's DMA runs.
+        hip_check(hipEventSynchronize(st.done[b]), "hipEventSynchronize (staging)");
+        st.copy(st.buf[b], static_cast<const char*>(src) + off, n);
+        hip_check(hipMemcpyAsync(static_cast<char*>(dst) + off, st.buf[b], n, hipMemcpyHostToDevice, m_stream),
+                  "hipMemcpyAsync H2D (staged)");
+        hip_check(hipEventRecord(st.done[b], m_stream), "hipEventRecord (staging)");
+    }
+    wait();
+}
+
+void HIPContext::copy_d2h(void* dst, const void* src, size_t bytes) {
+    if (bytes < kStagingMin) {
+        hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, m_stream), "hipMemcpyAsync D2H");
+        wait();
+        return;
+    }
+    std::lock_guard<std::mutex> lk(m_staging_mu);
+    Staging& st = staging();
+    // Chunk i's DMA is issued before chunk i-1 is copied out of its pinned buffer.
+    int prev = -1;
+    size_t prev_off = 0, prev_n = 0, i = 0;
+    auto drain = [&] {
+        hip_check(hipEventSynchronize(st.done[prev]), "hipEventSynchronize (staging)");
+        st.copy(static_cast<char*>(dst) + prev_off, st.buf[prev], prev_n);
+    };
+    for (size_t off = 0; off < bytes; off += Staging::kChunk, ++i) {
+        const size_t n = std::min(Staging::kChunk, bytes - off);
+        const int b = static_cast<int>(i & 1);
+        hip_check(hipMemcpyAsync(st.buf[b], static_cast<const char*>(src) + off, n, hipMemcpyDeviceToHost, m_stream),
+                  "hipMemcpyAsync D2H (staged)");
+        hip_check(hipEventRecord(st.done[b], m_stream), "hipEventRecord (staging)");
+        if (prev >= 0) drain();
+        prev = b;
+        prev_off = off;
+        prev_n = n;
+    }
+    if (prev >= 0) drain();
+    wait();
+}
 
 std::shared_ptr<HIPContext> HIPContext::get() {
     static std::mutex mu;
@@ -68,10 +217,7 @@ HIPTensor::HIPTensor(void* host_ptr, size_t numel, DataType dtype, std::shared_p
     const size_t bytes = numel * calc_dtype_size(dtype);
     hip_check(hipSetDevice(m_context->device_id()), "hipSetDevice");
     hip_check(hipMalloc(&m_data, bytes), "hipMalloc");
-    if (host_ptr) {
-        hip_check(hipMemcpyAsync(m_data, host_ptr, bytes, hipMemcpyHostToDevice, m_context->stream()), "hipMemcpyAsync H2D");
-        m_context->wait();
-    }
+    if (host_ptr) m_context->copy_h2d(m_data, host_ptr, bytes);
 }
 
 HIPTensor::~HIPTensor() {
@@ -154,15 +300,13 @@ void copy_device_to_host(std::shared_ptr<TensorImpl> src, std::shared_ptr<Tensor
     auto ctx = hip_ctx_of(src);
     // dst is sized to the tensor; src may be a larger storage whose leading elements are the tensor.
     const size_t bytes = dst->numel() * calc_dtype_size(dtype);
-    hip_check(hipMemcpyAsync(dst->data(), src->data(), bytes, hipMemcpyDeviceToHost, ctx->stream()), "hipMemcpyAsync D2H");
-    ctx->wait();
+    ctx->copy_d2h(dst->data(), src->data(), bytes);
 }
 
 void copy_host_to_device(std::shared_ptr<TensorImpl> src, std::shared_ptr<TensorImpl> dst, DataType dtype) {
     auto ctx = hip_ctx_of(dst);
     const size_t bytes = dst->numel() * calc_dtype_size(dtype);
-    hip_check(hipMemcpyAsync(dst->data(), src->data(), bytes, hipMemcpyHostToDevice, ctx->stream()), "hipMemcpyAsync H2D");
-    ctx->wait();
+    ctx->copy_h2d(dst->data(), src->data(), bytes);
 }
 
 // ---- registration (no GPU is touched until the first HIP tensor) --------------------------------
