@@ -215,6 +215,7 @@ EW = {
     "cast_c3a": "typecast bf16 -> fp32 of [16,2048,4096] (the CPU backend's widening of c3's A)",
     "random_c3a": "seeded uniform bf16 [16,2048,4096] (ops::Random on the device)",
     "fill_c3a": "fill fp32 [16,2048,4096] with 1.0 (ops::Ones on the device)",
+    "transpose_c4k": "ops::Transpose(K, {0,2,1}) materialised: fp16 [32,2048,128] -> [32,128,2048] (tv_hip_repack)",
 }
 
 
@@ -237,6 +238,18 @@ def run_ew(name: str, steps: int, warmup: int) -> dict:
         dst = torch.empty(n, dtype=torch.int16, device="cuda")
         call = lambda: L.tv_hip_random(ctypes.c_void_p(dst.data_ptr()), tv.BFLOAT16, n, -1.0, 1.0, 5, sh)  # noqa: E731
         nbytes = n * 2
+    elif name == "transpose_c4k":
+        m = 32 * 2048 * 128
+        src = torch.empty(m, dtype=torch.int16, device="cuda")  # K, fp16 storage
+        tv.check(L.tv_hip_random(ctypes.c_void_p(src.data_ptr()), tv.FLOAT16, m, -1.0, 1.0, 8, sh))
+        dst = torch.empty(m, dtype=torch.int16, device="cuda")
+        a = tv.TvRepackArgs()
+        a.ndim, a.elem_size = 3, 2
+        for d, (ext, st) in enumerate(zip((32, 128, 2048), (2048 * 128, 1, 128))):
+            a.shape[d], a.strides[d] = ext, st
+        a.src, a.dst = src.data_ptr(), dst.data_ptr()
+        call = lambda: L.tv_hip_repack(ctypes.byref(a), sh)  # noqa: E731
+        nbytes = m * 2 * 2
     else:
         dst = torch.empty(n, dtype=torch.float32, device="cuda")
         call = lambda: L.tv_hip_fill(ctypes.c_void_p(dst.data_ptr()), tv.FLOAT32, n, 1.0, sh)  # noqa: E731
@@ -318,7 +331,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="c1,c2,c3,c3_fused,c4,c5m1,c5m8,cast_c3a,random_c3a,fill_c3a")
+    ap.add_argument("--configs", default="c1,c2,c3,c3_fused,c4,c5m1,c5m8,cast_c3a,random_c3a,fill_c3a,transpose_c4k")
     ap.add_argument("--only", default=None,
                     help="run only this config's GPU kernel (for profilers); 'copy' runs the traffic calibration copy")
     ap.add_argument("--no-cpu", action="store_true")

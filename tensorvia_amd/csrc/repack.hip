@@ -1,7 +1,14 @@
-// Strided view -> contiguous copy (TensorImpl::clone_as_contiguous of the HIP backend).
-// Restates RepackImpl<Device::CUDA> (reference src/backend/cuda/repack.cu:5-54) without its
-// per-call device allocations: shape and strides travel in the kernel arguments.  Each thread
-// copies one element; consecutive threads write consecutive destination elements.
+// Strided view -> contiguous copy (TensorImpl::clone_as_contiguous of the HIP backend, and the
+// materialising ops::Transpose).  Restates RepackImpl<Device::CUDA> (reference
+// src/backend/cuda/repack.cu:5-54) without its per-call device allocations: shape and strides travel
+// in the kernel arguments.  Three kernels, by the view's layout:
+//  * rows: the innermost dimension is contiguous in the source and rows are 16-byte aligned; each
+//    thread moves 16 bytes, so reads and writes are whole 16-byte accesses;
+//  * transpose: the last two dimensions are swapped (source stride 1 on the next-to-last dimension,
+//    as K.permute(0, 2, 1)); 64 x 64 element tiles go through LDS, so reads run along the source's
+//    contiguous dimension and writes along the destination's;
+//  * element: anything else, one element per thread, consecutive threads writing consecutive
+//    destination elements.
 #include "tv_kernels.h"
 
 namespace tvk {
@@ -15,18 +22,84 @@ struct RepackDesc {
     void* dst;
 };
 
+// Source element offset of the first element of "outer" index o over dimensions [0, nd).
+__device__ inline int64_t outer_offset(const RepackDesc& r, int nd, int64_t o) {
+    int64_t off = 0;
+    for (int d = nd - 1; d >= 0; --d) {
+        const int64_t c = o % r.shape[d];
+        o /= r.shape[d];
+        off += c * r.strides[d];
+    }
+    return off;
+}
+
 template <typename E>
 __global__ __launch_bounds__(256) void repack_kernel(RepackDesc r) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < r.numel; i += stride) {
-        int64_t rem = i, off = 0;
-        for (int d = r.ndim - 1; d >= 0; --d) {
-            const int64_t c = rem % r.shape[d];
-            rem /= r.shape[d];
-            off += c * r.strides[d];
-        }
-        static_cast<E*>(r.dst)[i] = static_cast<const E*>(r.src)[off];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < r.numel; i += stride)
+        static_cast<E*>(r.dst)[i] = static_cast<const E*>(r.src)[outer_offset(r, r.ndim, i)];
+}
+
+// Rows of CPR 16-byte chunks: chunk c of destination row w comes from the row's source offset.
+__global__ __launch_bounds__(256) void repack_rows_kernel(RepackDesc r, int64_t rows, int cpr, int es) {
+    const int64_t total = rows * cpr;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int64_t w = i / cpr;
+        const int c = (int)(i - w * cpr);
+        const char* s = static_cast<const char*>(r.src) + outer_offset(r, r.ndim - 1, w) * es + (int64_t)c * 16;
+        *reinterpret_cast<u32x4*>(static_cast<char*>(r.dst) + i * 16) = *reinterpret_cast<const u32x4*>(s);
     }
+}
+
+// dst[o][i][j] = src[outer(o) + i + j * sC]: tiles of 64 (i) x 64 (j) elements.  Loads: lane l of a
+// tile row reads i = i0 + l % 64 (contiguous in the source); stores: lane l writes j = j0 + l % 64
+// (contiguous in the destination).  The LDS tile is padded by one element per row.
+template <typename E>
+__global__ __launch_bounds__(256) void repack_transpose_kernel(RepackDesc r, int64_t tiles_i, int64_t tiles_j) {
+    __shared__ E tile[64][65];
+    const int nd = r.ndim;
+    const int64_t R = r.shape[nd - 2], C = r.shape[nd - 1], sC = r.strides[nd - 1];
+    const int64_t per_outer = tiles_i * tiles_j;
+    const int64_t total = per_outer * (r.numel / (R * C));
+    const int l = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const E* src = static_cast<const E*>(r.src);
+    E* dst = static_cast<E*>(r.dst);
+    for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
+        const int64_t o = t / per_outer;
+        const int64_t rem = t - o * per_outer;
+        const int64_t i0 = (rem / tiles_j) * 64, j0 = (rem % tiles_j) * 64;
+        const int64_t base = outer_offset(r, nd - 2, o);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int jj = q + 4 * k;
+            if (i0 + l < R && j0 + jj < C) tile[jj][l] = src[base + (i0 + l) + (j0 + jj) * sC];
+        }
+        __syncthreads();
+        E* out = dst + o * R * C;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int ii = q + 4 * k;
+            if (i0 + ii < R && j0 + l < C) out[(i0 + ii) * C + j0 + l] = tile[l][ii];
+        }
+        __syncthreads();
+    }
+}
+
+static unsigned grid_for(int64_t items, int64_t per_block) {
+    int64_t blocks = (items + per_block - 1) / per_block;
+    if (blocks > 65536) blocks = 65536;
+    return (unsigned)(blocks < 1 ? 1 : blocks);
+}
+
+template <typename E>
+static int launch_transpose(const RepackDesc& r, hipStream_t stream) {
+    const int nd = r.ndim;
+    const int64_t R = r.shape[nd - 2], C = r.shape[nd - 1];
+    const int64_t tiles_i = (R + 63) / 64, tiles_j = (C + 63) / 64;
+    const int64_t total = tiles_i * tiles_j * (r.numel / (R * C));
+    hipLaunchKernelGGL(repack_transpose_kernel<E>, dim3(grid_for(total, 1)), dim3(256), 0, stream, r, tiles_i, tiles_j);
+    return hipGetLastError();
 }
 
 int launch_repack(const tv_repack_args* a, hipStream_t stream) {
@@ -41,14 +114,38 @@ int launch_repack(const tv_repack_args* a, hipStream_t stream) {
     r.src = a->src;
     r.dst = a->dst;
     if (r.numel == 0) return 0;
-    int64_t blocks = (r.numel + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    switch (a->elem_size) {
-        case 1: hipLaunchKernelGGL(repack_kernel<uint8_t>, dim3((unsigned)blocks), dim3(256), 0, stream, r); break;
-        case 2: hipLaunchKernelGGL(repack_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, stream, r); break;
-        case 4: hipLaunchKernelGGL(repack_kernel<uint32_t>, dim3((unsigned)blocks), dim3(256), 0, stream, r); break;
-        case 8: hipLaunchKernelGGL(repack_kernel<uint64_t>, dim3((unsigned)blocks), dim3(256), 0, stream, r); break;
-        default: return TV_E_DTYPE;
+    const int es = a->elem_size;
+    if (es != 1 && es != 2 && es != 4 && es != 8) return TV_E_DTYPE;
+    const int nd = r.ndim;
+
+    // Rows: contiguous innermost dimension in whole, aligned 16-byte chunks.
+    if (nd >= 1 && r.strides[nd - 1] == 1 && (r.shape[nd - 1] * es) % 16 == 0 &&
+        (reinterpret_cast<uintptr_t>(r.src) % 16) == 0 && (reinterpret_cast<uintptr_t>(r.dst) % 16) == 0) {
+        bool aligned = true;
+        for (int d = 0; d < nd - 1; ++d)
+            if (r.shape[d] > 1 && (r.strides[d] * es) % 16 != 0) aligned = false;
+        const int64_t cpr = r.shape[nd - 1] * es / 16;
+        if (aligned && cpr <= 0x7FFFFFFF) {
+            const int64_t rows = r.numel / r.shape[nd - 1];
+            hipLaunchKernelGGL(repack_rows_kernel, dim3(grid_for(rows * cpr, 256)), dim3(256), 0, stream, r, rows, (int)cpr, es);
+            return hipGetLastError();
+        }
+    }
+    // Transpose of the last two dimensions.
+    if (nd >= 2 && r.strides[nd - 2] == 1 && r.strides[nd - 1] != 1 && r.shape[nd - 2] > 1 && r.shape[nd - 1] > 1) {
+        switch (es) {
+            case 1: return launch_transpose<uint8_t>(r, stream);
+            case 2: return launch_transpose<uint16_t>(r, stream);
+            case 4: return launch_transpose<uint32_t>(r, stream);
+            default: return launch_transpose<uint64_t>(r, stream);
+        }
+    }
+    const unsigned blocks = grid_for(r.numel, 256);
+    switch (es) {
+        case 1: hipLaunchKernelGGL(repack_kernel<uint8_t>, dim3(blocks), dim3(256), 0, stream, r); break;
+        case 2: hipLaunchKernelGGL(repack_kernel<uint16_t>, dim3(blocks), dim3(256), 0, stream, r); break;
+        case 4: hipLaunchKernelGGL(repack_kernel<uint32_t>, dim3(blocks), dim3(256), 0, stream, r); break;
+        default: hipLaunchKernelGGL(repack_kernel<uint64_t>, dim3(blocks), dim3(256), 0, stream, r); break;
     }
     return hipGetLastError();
 }
