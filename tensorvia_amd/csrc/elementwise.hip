@@ -2,10 +2,13 @@
 // (FillImpl / ZerosImpl / OnesImpl) and the seeded counter-based generator behind ops::Random
 // (RandomImpl).  All three are HBM-bound streams over contiguous buffers.
 //
-// Layout of the work: a thread owns 8 consecutive elements.  When both buffers are 16-byte aligned
-// and hold whole 8-element groups, the group moves with one vector access per operand (8 * size
-// bytes: one to four 16-byte accesses); the ragged end and misaligned buffers take an element loop.
-// Grid: enough 256-thread workgroups for 8 waves per SIMD, grid-striding beyond that.
+// Layout of the work: a workgroup owns 2048 consecutive elements, a thread 8 of them.  When both
+// buffers are 16-byte aligned, a thread's 8 elements are 8 / V runs of V = 16 / (widest element size)
+// (at most 8) consecutive elements, and run a of thread t starts at element a * 256 V + t V of the
+// workgroup's range: every vector access of a wave covers one contiguous span (64 x 16 bytes on the
+// wider side), so each store instruction writes whole cache lines.  The ragged end and misaligned
+// buffers take an element loop.  Grid: enough 256-thread workgroups for 8 waves per SIMD,
+// grid-striding beyond that.
 #include "tv_kernels.h"
 
 namespace tvk {
@@ -33,12 +36,17 @@ template <typename S, typename D> __device__ inline D cast_elem(S s) {
 
 constexpr int kEwGroup = 8; // elements per thread
 constexpr int kEwThreads = 256;
+constexpr int64_t kEwBlock = (int64_t)kEwGroup * kEwThreads; // elements per workgroup step
 
-// One thread's elements; aligned to their size (at most 16 bytes) so the group moves with the
-// widest accesses the alignment allows.
-template <typename E> struct alignas(kEwGroup * sizeof(E) < 16 ? kEwGroup * sizeof(E) : 16) Group {
-    E v[kEwGroup];
+// V consecutive elements moved by one access (V * sizeof(E) bytes, aligned to that).
+template <typename E, int V> struct alignas(V * sizeof(E)) Run {
+    E v[V];
 };
+// Elements per run: 16 bytes of the wider element type, at most a thread's 8.
+template <int A, int B> constexpr int ew_run() {
+    constexpr int w = A > B ? A : B;
+    return 16 / w < kEwGroup ? 16 / w : kEwGroup;
+}
 
 static unsigned ew_blocks(int64_t n) {
     const int64_t groups = (n + kEwGroup - 1) / kEwGroup;
@@ -54,16 +62,21 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 template <typename S, typename D, bool VEC>
 __global__ __launch_bounds__(kEwThreads) void cast_kernel(const S* __restrict__ src, D* __restrict__ dst, int64_t n) {
-    const int64_t stride = (int64_t)gridDim.x * kEwThreads * kEwGroup;
-    for (int64_t i0 = ((int64_t)blockIdx.x * kEwThreads + threadIdx.x) * kEwGroup; i0 < n; i0 += stride) {
-        if (VEC && i0 + kEwGroup <= n) {
-            const Group<S> g = *reinterpret_cast<const Group<S>*>(src + i0);
-            Group<D> o;
+    constexpr int V = ew_run<sizeof(S), sizeof(D)>();
+    const int64_t stride = (int64_t)gridDim.x * kEwBlock;
+    for (int64_t b0 = (int64_t)blockIdx.x * kEwBlock; b0 < n; b0 += stride) {
 #pragma unroll
-            for (int e = 0; e < kEwGroup; ++e) o.v[e] = cast_elem<S, D>(g.v[e]);
-            *reinterpret_cast<Group<D>*>(dst + i0) = o;
-        } else {
-            for (int64_t i = i0; i < n && i < i0 + kEwGroup; ++i) dst[i] = cast_elem<S, D>(src[i]);
+        for (int a = 0; a < kEwGroup / V; ++a) {
+            const int64_t i0 = b0 + (int64_t)a * kEwThreads * V + (int64_t)threadIdx.x * V;
+            if (VEC && i0 + V <= n) {
+                const Run<S, V> g = *reinterpret_cast<const Run<S, V>*>(src + i0);
+                Run<D, V> o;
+#pragma unroll
+                for (int e = 0; e < V; ++e) o.v[e] = cast_elem<S, D>(g.v[e]);
+                *reinterpret_cast<Run<D, V>*>(dst + i0) = o;
+            } else {
+                for (int64_t i = i0; i < n && i < i0 + V; ++i) dst[i] = cast_elem<S, D>(src[i]);
+            }
         }
     }
 }
@@ -114,16 +127,21 @@ int launch_typecast(const void* src, int src_dt, void* dst, int dst_dt, int64_t 
 
 template <typename E, bool VEC>
 __global__ __launch_bounds__(kEwThreads) void fill_kernel(E* __restrict__ dst, int64_t n, float value) {
+    constexpr int V = ew_run<sizeof(E), sizeof(E)>();
     const E v = static_cast<E>(value); // T(val), reference initializer.cpp:14-17
-    const int64_t stride = (int64_t)gridDim.x * kEwThreads * kEwGroup;
-    for (int64_t i0 = ((int64_t)blockIdx.x * kEwThreads + threadIdx.x) * kEwGroup; i0 < n; i0 += stride) {
-        if (VEC && i0 + kEwGroup <= n) {
-            Group<E> o;
+    const int64_t stride = (int64_t)gridDim.x * kEwBlock;
+    for (int64_t b0 = (int64_t)blockIdx.x * kEwBlock; b0 < n; b0 += stride) {
 #pragma unroll
-            for (int e = 0; e < kEwGroup; ++e) o.v[e] = v;
-            *reinterpret_cast<Group<E>*>(dst + i0) = o;
-        } else {
-            for (int64_t i = i0; i < n && i < i0 + kEwGroup; ++i) dst[i] = v;
+        for (int a = 0; a < kEwGroup / V; ++a) {
+            const int64_t i0 = b0 + (int64_t)a * kEwThreads * V + (int64_t)threadIdx.x * V;
+            if (VEC && i0 + V <= n) {
+                Run<E, V> o;
+#pragma unroll
+                for (int e = 0; e < V; ++e) o.v[e] = v;
+                *reinterpret_cast<Run<E, V>*>(dst + i0) = o;
+            } else {
+                for (int64_t i = i0; i < n && i < i0 + V; ++i) dst[i] = v;
+            }
         }
     }
 }
@@ -166,15 +184,20 @@ template <typename E> __device__ inline E random_elem(const RandomArgs& r, int64
 
 template <typename E, bool VEC>
 __global__ __launch_bounds__(kEwThreads) void random_kernel(E* __restrict__ dst, int64_t n, RandomArgs r) {
-    const int64_t stride = (int64_t)gridDim.x * kEwThreads * kEwGroup;
-    for (int64_t i0 = ((int64_t)blockIdx.x * kEwThreads + threadIdx.x) * kEwGroup; i0 < n; i0 += stride) {
-        if (VEC && i0 + kEwGroup <= n) {
-            Group<E> o;
+    constexpr int V = ew_run<sizeof(E), sizeof(E)>();
+    const int64_t stride = (int64_t)gridDim.x * kEwBlock;
+    for (int64_t b0 = (int64_t)blockIdx.x * kEwBlock; b0 < n; b0 += stride) {
 #pragma unroll
-            for (int e = 0; e < kEwGroup; ++e) o.v[e] = random_elem<E>(r, i0 + e);
-            *reinterpret_cast<Group<E>*>(dst + i0) = o;
-        } else {
-            for (int64_t i = i0; i < n && i < i0 + kEwGroup; ++i) dst[i] = random_elem<E>(r, i);
+        for (int a = 0; a < kEwGroup / V; ++a) {
+            const int64_t i0 = b0 + (int64_t)a * kEwThreads * V + (int64_t)threadIdx.x * V;
+            if (VEC && i0 + V <= n) {
+                Run<E, V> o;
+#pragma unroll
+                for (int e = 0; e < V; ++e) o.v[e] = random_elem<E>(r, i0 + e);
+                *reinterpret_cast<Run<E, V>*>(dst + i0) = o;
+            } else {
+                for (int64_t i = i0; i < n && i < i0 + V; ++i) dst[i] = random_elem<E>(r, i);
+            }
         }
     }
 }
