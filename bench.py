@@ -212,7 +212,7 @@ def run_vendor(name: str, inp, steps: int, warmup: int) -> dict:
 
 # Element-wise device ops of the backend, on the c3 A operand's shape (134,217,728 elements).
 EW = {
-    "cast_c3a": "typecast bf16 -> fp32 of [16,2048,4096] (the CPU backend's widening of c3's A)",
+    "cast_c3a": "typecast bf16 -> fp32 of [16,2048,4096] (the CPU backend's widening of c3's A; 2 sources in turn)",
     "random_c3a": "seeded uniform bf16 [16,2048,4096] (ops::Random on the device)",
     "fill_c3a": "fill fp32 [16,2048,4096] with 1.0 (ops::Ones on the device)",
     "transpose_c4k": "ops::Transpose(K, {0,2,1}) materialised: fp16 [32,2048,128] -> [32,128,2048] (tv_hip_repack)",
@@ -228,11 +228,18 @@ def run_ew(name: str, steps: int, warmup: int) -> dict:
     n = 16 * 2048 * 4096
     sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     if name == "cast_c3a":
-        src = torch.empty(n, dtype=torch.int16, device="cuda")  # n bf16 elements (2-byte storage)
-        tv.check(L.tv_hip_random(ctypes.c_void_p(src.data_ptr()), tv.BFLOAT16, n, -1.0, 1.0, 5, sh))
+        # Two sources (2 x 268 MB) taken in turn, so that no call finds its source in the 256 MB
+        # MALL (Infinity Cache) from the call before.
+        srcs = [torch.empty(n, dtype=torch.int16, device="cuda") for _ in range(2)]  # bf16 storage
+        for s_ in srcs:
+            tv.check(L.tv_hip_random(ctypes.c_void_p(s_.data_ptr()), tv.BFLOAT16, n, -1.0, 1.0, 5, sh))
         dst = torch.empty(n, dtype=torch.float32, device="cuda")
-        call = lambda: L.tv_hip_typecast(ctypes.c_void_p(src.data_ptr()), tv.BFLOAT16,  # noqa: E731
-                                         ctypes.c_void_p(dst.data_ptr()), tv.FLOAT32, n, sh)
+        turn = [0]
+
+        def call():
+            turn[0] ^= 1
+            return L.tv_hip_typecast(ctypes.c_void_p(srcs[turn[0]].data_ptr()), tv.BFLOAT16,
+                                     ctypes.c_void_p(dst.data_ptr()), tv.FLOAT32, n, sh)
         nbytes = n * 2 + n * 4
     elif name == "random_c3a":
         dst = torch.empty(n, dtype=torch.int16, device="cuda")

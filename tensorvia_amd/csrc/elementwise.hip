@@ -73,7 +73,11 @@ __global__ __launch_bounds__(kEwThreads) void cast_kernel(const S* __restrict__ 
                 Run<D, V> o;
 #pragma unroll
                 for (int e = 0; e < V; ++e) o.v[e] = cast_elem<S, D>(g.v[e]);
-                *reinterpret_cast<Run<D, V>*>(dst + i0) = o;
+                // Streaming (nt sc1) stores when a run is 16 bytes: a wave's store is whole lines,
+                // and the output does not evict the source from the caches (cast_c3a 140 -> 134 us;
+                // the same policy on fill measured 2 % slower and is not used there).
+                if constexpr (sizeof(Run<D, V>) == 16) store_stream16(dst + i0, __builtin_bit_cast(u32x4, o));
+                else *reinterpret_cast<Run<D, V>*>(dst + i0) = o;
             } else {
                 for (int64_t i = i0; i < n && i < i0 + V; ++i) dst[i] = cast_elem<S, D>(src[i]);
             }
