@@ -172,8 +172,9 @@ struct RandomArgs {
     uint64_t range;  // hi - lo + 1
 };
 
-template <typename E> __device__ inline E random_elem(const RandomArgs& r, int64_t i) {
-    const uint64_t z = mix64(r.key + (uint64_t)(i + 1) * kGamma);
+// Element whose SplitMix64 state (key + (i + 1) * G) is z0.
+template <typename E> __device__ inline E random_from_state(const RandomArgs& r, uint64_t z0) {
+    const uint64_t z = mix64(z0);
     if constexpr (__is_same(E, int8_t) || __is_same(E, int16_t) || __is_same(E, int32_t) || __is_same(E, int64_t)) {
         return static_cast<E>(r.lo + (int64_t)(((z >> 32) * r.range) >> 32));
     } else {
@@ -186,6 +187,10 @@ template <typename E> __device__ inline E random_elem(const RandomArgs& r, int64
     }
 }
 
+template <typename E> __device__ inline E random_elem(const RandomArgs& r, int64_t i) {
+    return random_from_state<E>(r, r.key + (uint64_t)(i + 1) * kGamma);
+}
+
 template <typename E, bool VEC>
 __global__ __launch_bounds__(kEwThreads) void random_kernel(E* __restrict__ dst, int64_t n, RandomArgs r) {
     constexpr int V = ew_run<sizeof(E), sizeof(E)>();
@@ -195,9 +200,11 @@ __global__ __launch_bounds__(kEwThreads) void random_kernel(E* __restrict__ dst,
         for (int a = 0; a < kEwGroup / V; ++a) {
             const int64_t i0 = b0 + (int64_t)a * kEwThreads * V + (int64_t)threadIdx.x * V;
             if (VEC && i0 + V <= n) {
+                // Consecutive states differ by G: one 64-bit multiply per run, then additions.
                 Run<E, V> o;
+                uint64_t z0 = r.key + (uint64_t)(i0 + 1) * kGamma;
 #pragma unroll
-                for (int e = 0; e < V; ++e) o.v[e] = random_elem<E>(r, i0 + e);
+                for (int e = 0; e < V; ++e, z0 += kGamma) o.v[e] = random_from_state<E>(r, z0);
                 *reinterpret_cast<Run<E, V>*>(dst + i0) = o;
             } else {
                 for (int64_t i = i0; i < n && i < i0 + V; ++i) dst[i] = random_elem<E>(r, i);
