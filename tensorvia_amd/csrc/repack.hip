@@ -6,7 +6,8 @@
 //    thread moves 16 bytes, so reads and writes are whole 16-byte accesses;
 //  * transpose: the last two dimensions are swapped (source stride 1 on the next-to-last dimension,
 //    as K.permute(0, 2, 1)); 64 x 64 element tiles go through LDS, so reads run along the source's
-//    contiguous dimension and writes along the destination's;
+//    contiguous dimension and writes along the destination's (16-bit elements in 4-byte pairs when
+//    the view allows);
 //  * element: anything else, one element per thread, consecutive threads writing consecutive
 //    destination elements.
 #include "tv_kernels.h"
@@ -86,6 +87,46 @@ __global__ __launch_bounds__(256) void repack_transpose_kernel(RepackDesc r, int
     }
 }
 
+// 16-bit elements moved in pairs: the same tiles, with 4-byte loads of two consecutive i and 4-byte
+// stores of two consecutive j.  Requires even R and C, even outer strides and 4-byte aligned
+// buffers (checked by the launcher), so every pair lies inside the view and is aligned.
+__global__ __launch_bounds__(256) void repack_transpose16_kernel(RepackDesc r, int64_t tiles_i, int64_t tiles_j) {
+    __shared__ uint16_t tile[64][66];
+    const int nd = r.ndim;
+    const int64_t R = r.shape[nd - 2], C = r.shape[nd - 1], sC = r.strides[nd - 1];
+    const int64_t per_outer = tiles_i * tiles_j;
+    const int64_t total = per_outer * (r.numel / (R * C));
+    const int p = threadIdx.x & 31, q = threadIdx.x >> 5; // pair index, row group (8)
+    const uint16_t* src = static_cast<const uint16_t*>(r.src);
+    uint16_t* dst = static_cast<uint16_t*>(r.dst);
+    for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
+        const int64_t o = t / per_outer;
+        const int64_t rem = t - o * per_outer;
+        const int64_t i0 = (rem / tiles_j) * 64, j0 = (rem % tiles_j) * 64;
+        const int64_t base = outer_offset(r, nd - 2, o);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int jj = q + 8 * k;
+            if (i0 + 2 * p < R && j0 + jj < C) {
+                const unsigned v = *reinterpret_cast<const unsigned*>(src + base + (i0 + 2 * p) + (j0 + jj) * sC);
+                tile[jj][2 * p] = (uint16_t)(v & 0xFFFFu);
+                tile[jj][2 * p + 1] = (uint16_t)(v >> 16);
+            }
+        }
+        __syncthreads();
+        uint16_t* out = dst + o * R * C;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int ii = q + 8 * k;
+            if (i0 + ii < R && j0 + 2 * p < C) {
+                const unsigned v = (unsigned)tile[2 * p][ii] | ((unsigned)tile[2 * p + 1][ii] << 16);
+                *reinterpret_cast<unsigned*>(out + (i0 + ii) * C + j0 + 2 * p) = v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 static unsigned grid_for(int64_t items, int64_t per_block) {
     int64_t blocks = (items + per_block - 1) / per_block;
     if (blocks > 65536) blocks = 65536;
@@ -98,6 +139,16 @@ static int launch_transpose(const RepackDesc& r, hipStream_t stream) {
     const int64_t R = r.shape[nd - 2], C = r.shape[nd - 1];
     const int64_t tiles_i = (R + 63) / 64, tiles_j = (C + 63) / 64;
     const int64_t total = tiles_i * tiles_j * (r.numel / (R * C));
+    if constexpr (sizeof(E) == 2) {
+        bool pairs = R % 2 == 0 && C % 2 == 0 && r.strides[nd - 1] % 2 == 0 &&
+                     (reinterpret_cast<uintptr_t>(r.src) % 4) == 0 && (reinterpret_cast<uintptr_t>(r.dst) % 4) == 0;
+        for (int d = 0; d < nd - 2; ++d)
+            if (r.shape[d] > 1 && r.strides[d] % 2 != 0) pairs = false;
+        if (pairs) {
+            hipLaunchKernelGGL(repack_transpose16_kernel, dim3(grid_for(total, 1)), dim3(256), 0, stream, r, tiles_i, tiles_j);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL(repack_transpose_kernel<E>, dim3(grid_for(total, 1)), dim3(256), 0, stream, r, tiles_i, tiles_j);
     return hipGetLastError();
 }
