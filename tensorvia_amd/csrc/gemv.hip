@@ -19,12 +19,14 @@
 //  * x's slice is staged in LDS once per workgroup (while the first W loads are in flight);
 //  * products use the packed dot instructions over row pairs / quads of W, with the pairs built by
 //    v_perm_b32: v_dot2_f32_bf16 / v_dot2_f32_f16 (fp32 accumulation), v_dot4_i32_i8 (exact int32
-//    accumulation); fp32 uses fp32 FMA;
+//    accumulation); fp32 uses fp32 FMA.  16-bit W at M >= 3 goes to gemv_mfma_kernel instead
+//    (matrix cores, W transposed through LDS), since the dot loop is VALU-bound there;
 //  * the k-lanes are summed through LDS in a fixed order;
 //  * with S > 1 each workgroup publishes its strip partial to slot s (agent-coherent stores) and
 //    counts itself in with an agent-scope atomic; the workgroup that arrives last sums slots
 //    0..S-1 in order (deterministic), writes C and resets the counter.  No workgroup waits for
 //    another, and there is no second kernel.
+#include "gemm_mfma_impl.h"
 #include "tv_kernels.h"
 
 namespace tvk {
@@ -303,6 +305,165 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
     if (tid == 0) __hip_atomic_store(g.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Matrix-core variant for 16-bit W at M up to 8 (the dot-product loop above is VALU-bound there:
+// 16 v_dot2 per x row per 64 bytes of W).  Same strips (64 columns, 128 bytes of each W row), K
+// slices and slot combine; inside a workgroup, the 4 waves take 32-row chunks of the slice in turn
+// (chunk c goes to wave c mod 4):
+//  * a chunk is 4 KB: 4 nontemporal 16-byte buffer loads per lane (lane l: rows l/8 + 8q, columns
+//    8 (l mod 8) ..), DEPTH chunks in flight per wave;
+//  * the wave writes it to its own LDS tile (32 rows x 64 columns, row pitch 144 bytes) and reads it
+//    back with ds_read_b64_tr_b16, which hands lane l the 8 consecutive rows of one column that the
+//    matrix core's B operand wants (column 16 f + l mod 16, rows 8 (l / 16) ..);
+//  * one v_mfma_f32_16x16x32 per 16 columns: A = x rows 0..15 (rows 8..15 and rows >= M are zero),
+//    so D[m][n] lands in lane n mod 16 + 16 (m / 4), element m mod 4;
+//  * the waves' partials are summed through LDS in wave order, then published as in gemv_kernel.
+// A wave's LDS tile is private to it: LDS instructions of one wave execute in order, so the next
+// chunk's stores cannot overtake the previous chunk's reads.
+constexpr int kGemvMfmaPitch = 144;
+
+template <typename T>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs g) {
+    constexpr int ES = 2, VEC = 8, NB = 64, CH = 32, DEPTH = kGemvDepth, PITCH = kGemvMfmaPitch;
+    const GemmDesc& d = g.d;
+
+    extern __shared__ __attribute__((aligned(16))) char xs[]; // 8 rows x kpad x ES (launch size)
+    __shared__ __attribute__((aligned(16))) char wt[4][CH * PITCH];
+    __shared__ float red[4][8][NB];
+    __shared__ int last_flag;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lin = xcd_remap(blockIdx.x, gridDim.x);
+    const int b = lin / g.nblk;
+    const int n0 = (lin - b * g.nblk) * NB;
+    const int s = blockIdx.y;
+    const int k0 = s * g.kslice;
+    const int ks = min(d.K - k0, g.kslice);  // a multiple of VEC
+    const int nch = (ks + CH - 1) / CH;
+    const int kpad = nch * CH;
+    const int niter = (nch - wave + 3) / 4;  // chunks wave, wave + 4, ...
+
+    const int64_t rowb = d.sb_k * ES;
+    const char* wbase = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)k0 * d.sb_k) * ES;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wbase, (int64_t)(ks - 1) * rowb + (int64_t)d.N * ES);
+    const int r0 = lane >> 3, cc = lane & 7;
+    const int col = n0 + cc * VEC;
+    const bool col_ok = col < d.N; // N % VEC == 0 is a launch precondition
+    const unsigned colb = (unsigned)(col * ES);
+
+    u32x4 w[DEPTH][4];
+    auto issue = [&](int slot, int j) {
+        const int c = wave + 4 * j;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = c * CH + r0 + 8 * q;
+            const bool ok = col_ok && j < niter && r < ks; // rows past the slice read as zeros
+            w[slot][q] = buf_load16_nt(wr, ok ? (unsigned)(r * rowb) + colb : kOOB);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) issue(j, j);
+
+    // x[b][0..8)[k0 .. k0 + kpad) in LDS; rows >= M and columns >= ks are zero.
+    {
+        const char* xb = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + k0) * ES;
+        const int cpr = kpad * ES / 16;
+        for (int i = tid; i < 8 * cpr; i += 256) {
+            const int m = i / cpr, c = i - m * cpr;
+            u32x4 v = {0, 0, 0, 0};
+            if (m < d.M && c * 16 < ks * ES) v = *reinterpret_cast<const u32x4*>(xb + (int64_t)m * d.sa_m * ES + c * 16);
+            *reinterpret_cast<u32x4*>(xs + m * kpad * ES + c * 16) = v;
+        }
+    }
+    __syncthreads();
+
+    f32x4 acc[4];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) acc[f] = f32x4{0, 0, 0, 0};
+    char* wl = wt[wave];
+    const int wr_off = r0 * PITCH + cc * 16;
+    const int rd_off = (8 * (lane >> 4) + ((lane & 15) >> 2)) * PITCH + 8 * (lane & 3);
+    const bool arow = (lane & 15) < 8;
+    const char* xa = xs + (lane & 7) * kpad * ES + (lane >> 4) * 8 * ES;
+    for (int j0 = 0; j0 < niter; j0 += DEPTH) {
+#pragma unroll
+        for (int dd = 0; dd < DEPTH; ++dd) {
+            const int j = j0 + dd;
+            if (j < niter) {
+                const int c = wave + 4 * j;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(wl + wr_off + q * 8 * PITCH) = w[dd][q];
+                u32x4 a = *reinterpret_cast<const u32x4*>(xa + c * CH * ES);
+                if (!arow) a = u32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int f = 0; f < 4; ++f) {
+                    const lds_char* p = (const lds_char*)(wl + rd_off + f * 16 * ES);
+                    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
+                    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * PITCH));
+                    const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+                    Mfma<T>::run(a, u32x4{l2.x, l2.y, h2.x, h2.y}, acc[f]);
+                }
+                if (j + DEPTH < niter) issue(dd, j + DEPTH);
+            }
+        }
+    }
+
+    // Wave partials D[m][n] (m < 8: lanes 0..31) to red, then sum the waves in order.
+    if (lane < 32)
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][4 * (lane >> 4) + r][16 * f + (lane & 15)] = acc[f][r];
+    __syncthreads();
+    float v[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int o = tid + 256 * i, m = o / NB, c = o % NB;
+        v[i] = ((red[0][m][c] + red[1][m][c]) + red[2][m][c]) + red[3][m][c];
+    }
+
+    const size_t csz = dtype_size(d.dtype_c);
+    char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
+    if (g.nslices == 1) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int o = tid + 256 * i, m = o / NB, c = o % NB;
+            if (m < d.M && n0 + c < d.N)
+                gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + c) * d.sc_n, d.dtype_c, gemv_epilogue(v[i], d, b, m, n0 + c));
+        }
+        return;
+    }
+
+    // Publish slot s of this strip ([8][NB] floats), count in; the last arriver sums the slots in order.
+    const int strip = lin;
+    float* slots = static_cast<float*>(g.part) + (int64_t)strip * g.nslices * 8 * NB;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        __hip_atomic_store(slots + (int64_t)s * 8 * NB + tid + 256 * i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads(); // every partial store of this workgroup has completed (s_waitcnt before s_barrier)
+    if (tid == 0)
+        last_flag = __hip_atomic_fetch_add(g.cnt + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g.nslices - 1;
+    __syncthreads();
+    if (!last_flag) return;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int o = tid + 256 * i, m = o / NB, c = o % NB;
+        if (m < d.M && n0 + c < d.N) {
+            float part_v[kGemvMaxSlices];
+#pragma unroll
+            for (int k = 0; k < kGemvMaxSlices; ++k)
+                part_v[k] = k < g.nslices ? __hip_atomic_load(slots + (int64_t)k * 8 * NB + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                          : 0.0f;
+            float t = part_v[0];
+#pragma unroll
+            for (int k = 1; k < kGemvMaxSlices; ++k)
+                if (k < g.nslices) t += part_v[k];
+            gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + c) * d.sc_n, d.dtype_c, gemv_epilogue(t, d, b, m, n0 + c));
+        }
+    }
+    if (tid == 0) __hip_atomic_store(g.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+
 __global__ __launch_bounds__(256) void gemv_zero_kernel(int* p, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
 }
@@ -441,6 +602,45 @@ static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices) {
     return hipGetLastError();
 }
 
+// The matrix-core GEMV (bf16 / fp16, 64-column strips): same K-slice rule as gemv_run.
+template <typename T>
+static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices) {
+    constexpr int NB = 64, VEC = 8, ES = 2, KCAP = gemv_kcap<T>();
+    if (d.K < 1) return TV_E_UNSUPPORTED;
+    const int nblk = (d.N + NB - 1) / NB;
+    int S = nslices < 1 ? 1 : nslices;
+    const int min_s = (d.K + KCAP - 1) / KCAP;
+    if (S < min_s) S = min_s;
+    int kslice = (d.K + S - 1) / S;
+    kslice = (kslice + VEC - 1) / VEC * VEC;
+    if (kslice > KCAP) kslice = KCAP;
+    S = (d.K + kslice - 1) / kslice;
+    if (S > kGemvMaxSlices) return TV_E_UNSUPPORTED;
+    if ((int64_t)(kslice - 1) * d.sb_k * ES + (int64_t)d.N * ES >= ((int64_t)1 << 30)) return TV_E_UNSUPPORTED;
+    const int64_t nwg = (int64_t)nblk * d.batch;
+    if (nwg > 0x7FFFFFFF || S > 65535) return TV_E_SHAPE;
+
+    GemvArgs g;
+    g.d = d;
+    g.kslice = kslice;
+    g.nslices = S;
+    g.nblk = nblk;
+    g.cnt = nullptr;
+    g.part = nullptr;
+    if (S > 1) {
+        void* cnt = nullptr;
+        int rc = get_workspace(stream, (size_t)nwg * sizeof(int), &cnt, 1);
+        if (rc) return rc;
+        rc = get_workspace(stream, (size_t)nwg * S * 8 * NB * sizeof(float), &g.part, 2);
+        if (rc) return rc;
+        g.cnt = static_cast<int*>(cnt);
+    }
+    const int kpad = (kslice + 31) / 32 * 32; // at most KCAP, a multiple of 32
+    hipLaunchKernelGGL(gemv_mfma_kernel<T>, dim3((unsigned)nwg, S), dim3(256), (size_t)8 * kpad * ES, stream, g);
+    return hipGetLastError();
+}
+
+
 template <typename T, int MR>
 static int gemv_dispatch_nl(const GemmDesc& d, hipStream_t stream, const GemvPlan& p) {
     if (p.threads == 256) {
@@ -478,8 +678,26 @@ int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads,
     }
 }
 
+// The matrix-core kernel serves 16-bit W at M >= 3 with whole 128-byte strips (N >= 64).  On c5's
+// W (bf16 [4096, 11008]) it is ahead by 21 % at M = 8 and 7 % at M = 4, level at M = 2 and 3 %
+// behind at M = 1 (dot-product kernel 25.8 / 20.8 / 19.7 / 19.1 us).  Its slices: about 688
+// workgroups in all (172 strips x 4 measured best among 1-12 slices), at least what x's LDS slice
+// needs, and no more than leaves each wave two 32-row chunks per slice.
+static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream) {
+    const int64_t strips = (int64_t)(d.N + 63) / 64 * d.batch;
+    const int max_s = d.K / 256 > 1 ? d.K / 256 : 1;
+    int s = (int)((688 + strips - 1) / strips);
+    if (s > max_s) s = max_s;
+    if (s > kGemvMaxSlices) s = kGemvMaxSlices;
+    // gemv_mfma_run raises s to what x's LDS slice needs
+    return d.dtype_a == TV_BFLOAT16 ? gemv_mfma_run<__bf16>(d, stream, s) : gemv_mfma_run<_Float16>(d, stream, s);
+}
+
 int launch_gemv(const GemmDesc& d, hipStream_t stream) {
     if (!gemv_layout_ok(d)) return TV_E_UNSUPPORTED;
+    if (d.N == 0 || d.batch == 0) return 0;
+    if ((d.dtype_a == TV_BFLOAT16 || d.dtype_a == TV_FLOAT16) && d.M >= 3 && gemv_nl(d) == 8)
+        return launch_gemv_mfma(d, stream);
     const GemvPlan p = gemv_plan(d);
     return launch_gemv_plan(d, stream, p.nl, p.threads, p.nslices);
 }

@@ -31,7 +31,7 @@ def test_config5_bf16_full_size(hip, M):
 
 @pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, FLOAT32, INT8])
 @pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
-@pytest.mark.parametrize("KN", [(64, 128), (4096, 1008), (1024, 11008), (16, 32)])
+@pytest.mark.parametrize("KN", [(64, 128), (4096, 1008), (1024, 11008), (16, 32), (208, 144), (4000, 1008)])
 def test_gemv_integer_inputs_exact(hip, dt, M, KN):
     K, N = KN
     if dt == INT8:
@@ -67,8 +67,9 @@ def test_gemv_uniform_vs_oracle(hip, dt):
     (assert_fp32_close if dt == FLOAT32 else assert_half_close)(c, ref, bound, K)
 
 
-def test_gemv_batched_and_broadcast(hip):
-    Bt, M, K, N = 3, 2, 512, 256
+@pytest.mark.parametrize("M", [2, 6], ids=["dot", "mfma"])
+def test_gemv_batched_and_broadcast(hip, M):
+    Bt, K, N = 3, 520, 264
     x = rng.uniform_int(42, Bt * M * K, -2, 2).astype(np.float32).reshape(Bt, M, K)
     w = rng.uniform_int(43, K * N, -2, 2).astype(np.float32).reshape(K, N)
     xb, wb = rng.f32_to_bf16_bits(x), rng.f32_to_bf16_bits(w)
