@@ -19,8 +19,8 @@
 //  * x's slice is staged in LDS once per workgroup (while the first W loads are in flight);
 //  * products use the packed dot instructions over row pairs / quads of W, with the pairs built by
 //    v_perm_b32: v_dot2_f32_bf16 / v_dot2_f32_f16 (fp32 accumulation), v_dot4_i32_i8 (exact int32
-//    accumulation); fp32 uses fp32 FMA.  16-bit W at M >= 3 goes to gemv_mfma_kernel instead
-//    (matrix cores, W transposed through LDS), since the dot loop is VALU-bound there;
+//    accumulation); fp32 uses fp32 FMA.  16-bit W with N >= 64 goes to gemv_mfma_kernel instead
+//    (matrix cores, W transposed through LDS), which is VALU-light and faster at every M;
 //  * the k-lanes are summed through LDS in a fixed order;
 //  * with S > 1 each workgroup publishes its strip partial to slot s (agent-coherent stores) and
 //    counts itself in with an agent-scope atomic; the workgroup that arrives last sums slots
@@ -305,10 +305,10 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
     if (tid == 0) __hip_atomic_store(g.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Matrix-core variant for 16-bit W at M up to 8 (the dot-product loop above is VALU-bound there:
-// 16 v_dot2 per x row per 64 bytes of W).  Same strips (64 columns, 128 bytes of each W row), K
-// slices and slot combine; inside a workgroup, the 4 waves take 32-row chunks of the slice in turn
-// (chunk c goes to wave c mod 4):
+// Matrix-core variant for 16-bit W (the dot-product loop above is VALU-bound at larger M: 16 v_dot2
+// per x row per 64 bytes of W).  Same strips (64 columns, 128 bytes of each W row), K slices and
+// slot combine; inside a workgroup, the WAVES waves take 32-row chunks of the slice in turn (chunk
+// c goes to wave c mod WAVES):
 //  * a chunk is 4 KB: 4 nontemporal 16-byte buffer loads per lane (lane l: rows l/8 + 8q, columns
 //    8 (l mod 8) ..), DEPTH chunks in flight per wave;
 //  * the wave writes it to its own LDS tile (32 rows x 64 columns, row pitch 144 bytes) and reads it
@@ -320,15 +320,17 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
 // A wave's LDS tile is private to it: LDS instructions of one wave execute in order, so the next
 // chunk's stores cannot overtake the previous chunk's reads.
 constexpr int kGemvMfmaPitch = 144;
+constexpr int kGemvMfmaWaves = 4, kGemvMfmaDepth = 2; // best of 2/4/8 waves x 1-8 chunks on c5's W
 
-template <typename T>
-__global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs g) {
-    constexpr int ES = 2, VEC = 8, NB = 64, CH = 32, DEPTH = kGemvDepth, PITCH = kGemvMfmaPitch;
+template <typename T, int WAVES, int DEPTH>
+__global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
+    constexpr int ES = 2, VEC = 8, NB = 64, CH = 32, PITCH = kGemvMfmaPitch, THREADS = WAVES * 64;
+    static_assert(8 * NB % THREADS == 0, "outputs per thread");
     const GemmDesc& d = g.d;
 
     extern __shared__ __attribute__((aligned(16))) char xs[]; // 8 rows x kpad x ES (launch size)
-    __shared__ __attribute__((aligned(16))) char wt[4][CH * PITCH];
-    __shared__ float red[4][8][NB];
+    __shared__ __attribute__((aligned(16))) char wt[WAVES][CH * PITCH];
+    __shared__ float red[WAVES][8][NB];
     __shared__ int last_flag;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -340,7 +342,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs g) {
     const int ks = min(d.K - k0, g.kslice);  // a multiple of VEC
     const int nch = (ks + CH - 1) / CH;
     const int kpad = nch * CH;
-    const int niter = (nch - wave + 3) / 4;  // chunks wave, wave + 4, ...
+    const int niter = (nch - wave + WAVES - 1) / WAVES; // chunks wave, wave + WAVES, ...
 
     const int64_t rowb = d.sb_k * ES;
     const char* wbase = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)k0 * d.sb_k) * ES;
@@ -352,7 +354,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs g) {
 
     u32x4 w[DEPTH][4];
     auto issue = [&](int slot, int j) {
-        const int c = wave + 4 * j;
+        const int c = wave + WAVES * j;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int r = c * CH + r0 + 8 * q;
@@ -367,7 +369,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs g) {
     {
         const char* xb = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + k0) * ES;
         const int cpr = kpad * ES / 16;
-        for (int i = tid; i < 8 * cpr; i += 256) {
+        for (int i = tid; i < 8 * cpr; i += THREADS) {
             const int m = i / cpr, c = i - m * cpr;
             u32x4 v = {0, 0, 0, 0};
             if (m < d.M && c * 16 < ks * ES) v = *reinterpret_cast<const u32x4*>(xb + (int64_t)m * d.sa_m * ES + c * 16);
@@ -389,7 +391,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs g) {
         for (int dd = 0; dd < DEPTH; ++dd) {
             const int j = j0 + dd;
             if (j < niter) {
-                const int c = wave + 4 * j;
+                const int c = wave + WAVES * j;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(wl + wr_off + q * 8 * PITCH) = w[dd][q];
                 u32x4 a = *reinterpret_cast<const u32x4*>(xa + c * CH * ES);
@@ -414,19 +416,23 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs g) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[wave][4 * (lane >> 4) + r][16 * f + (lane & 15)] = acc[f][r];
     __syncthreads();
-    float v[2];
+    constexpr int OPT = 8 * NB / THREADS; // outputs per thread
+    float v[OPT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int o = tid + 256 * i, m = o / NB, c = o % NB;
-        v[i] = ((red[0][m][c] + red[1][m][c]) + red[2][m][c]) + red[3][m][c];
+    for (int i = 0; i < OPT; ++i) {
+        const int o = tid + THREADS * i, m = o / NB, c = o % NB;
+        float t = red[0][m][c];
+#pragma unroll
+        for (int wv = 1; wv < WAVES; ++wv) t += red[wv][m][c];
+        v[i] = t;
     }
 
     const size_t csz = dtype_size(d.dtype_c);
     char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
     if (g.nslices == 1) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int o = tid + 256 * i, m = o / NB, c = o % NB;
+        for (int i = 0; i < OPT; ++i) {
+            const int o = tid + THREADS * i, m = o / NB, c = o % NB;
             if (m < d.M && n0 + c < d.N)
                 gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + c) * d.sc_n, d.dtype_c, gemv_epilogue(v[i], d, b, m, n0 + c));
         }
@@ -437,16 +443,16 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs g) {
     const int strip = lin;
     float* slots = static_cast<float*>(g.part) + (int64_t)strip * g.nslices * 8 * NB;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-        __hip_atomic_store(slots + (int64_t)s * 8 * NB + tid + 256 * i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < OPT; ++i)
+        __hip_atomic_store(slots + (int64_t)s * 8 * NB + tid + THREADS * i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads(); // every partial store of this workgroup has completed (s_waitcnt before s_barrier)
     if (tid == 0)
         last_flag = __hip_atomic_fetch_add(g.cnt + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g.nslices - 1;
     __syncthreads();
     if (!last_flag) return;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int o = tid + 256 * i, m = o / NB, c = o % NB;
+    for (int i = 0; i < OPT; ++i) {
+        const int o = tid + THREADS * i, m = o / NB, c = o % NB;
         if (m < d.M && n0 + c < d.N) {
             float part_v[kGemvMaxSlices];
 #pragma unroll
@@ -603,7 +609,7 @@ static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices) {
 }
 
 // The matrix-core GEMV (bf16 / fp16, 64-column strips): same K-slice rule as gemv_run.
-template <typename T>
+template <typename T, int WAVES = kGemvMfmaWaves, int DEPTH = kGemvMfmaDepth>
 static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices) {
     constexpr int NB = 64, VEC = 8, ES = 2, KCAP = gemv_kcap<T>();
     if (d.K < 1) return TV_E_UNSUPPORTED;
@@ -636,7 +642,7 @@ static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices) {
         g.cnt = static_cast<int*>(cnt);
     }
     const int kpad = (kslice + 31) / 32 * 32; // at most KCAP, a multiple of 32
-    hipLaunchKernelGGL(gemv_mfma_kernel<T>, dim3((unsigned)nwg, S), dim3(256), (size_t)8 * kpad * ES, stream, g);
+    hipLaunchKernelGGL((gemv_mfma_kernel<T, WAVES, DEPTH>), dim3((unsigned)nwg, S), dim3(WAVES * 64), (size_t)8 * kpad * ES, stream, g);
     return hipGetLastError();
 }
 
@@ -678,11 +684,11 @@ int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads,
     }
 }
 
-// The matrix-core kernel serves 16-bit W at M >= 3 with whole 128-byte strips (N >= 64).  On c5's
-// W (bf16 [4096, 11008]) it is ahead by 21 % at M = 8 and 7 % at M = 4, level at M = 2 and 3 %
-// behind at M = 1 (dot-product kernel 25.8 / 20.8 / 19.7 / 19.1 us).  Its slices: about 688
-// workgroups in all (172 strips x 4 measured best among 1-12 slices), at least what x's LDS slice
-// needs, and no more than leaves each wave two 32-row chunks per slice.
+// The matrix-core kernel serves 16-bit W with whole 128-byte strips (N >= 64).  On c5's W (bf16
+// [4096, 11008]) it takes 18.7 / 19.3 / 20.2 us at M = 1 / 4 / 8 against the dot-product kernel's
+// 19.2 / 20.9 / 25.7 us.  Its slices: about 688 workgroups in all (172 strips x 4 measured best
+// among 1-12 slices), at least what x's LDS slice needs, and no more than leaves each wave two
+// 32-row chunks per slice.
 static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream) {
     const int64_t strips = (int64_t)(d.N + 63) / 64 * d.batch;
     const int max_s = d.K / 256 > 1 ? d.K / 256 : 1;
@@ -696,7 +702,7 @@ static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream) {
 int launch_gemv(const GemmDesc& d, hipStream_t stream) {
     if (!gemv_layout_ok(d)) return TV_E_UNSUPPORTED;
     if (d.N == 0 || d.batch == 0) return 0;
-    if ((d.dtype_a == TV_BFLOAT16 || d.dtype_a == TV_FLOAT16) && d.M >= 3 && gemv_nl(d) == 8)
+    if ((d.dtype_a == TV_BFLOAT16 || d.dtype_a == TV_FLOAT16) && gemv_nl(d) == 8)
         return launch_gemv_mfma(d, stream);
     const GemvPlan p = gemv_plan(d);
     return launch_gemv_plan(d, stream, p.nl, p.threads, p.nslices);
