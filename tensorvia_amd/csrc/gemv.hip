@@ -439,12 +439,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
         return;
     }
 
-    // Publish slot s of this strip ([8][NB] floats), count in; the last arriver sums the slots in order.
+    // Publish slot s of this strip ([8][NB] floats, rows < M), count in; the last arriver sums the
+    // slots in order.
     const int strip = lin;
     float* slots = static_cast<float*>(g.part) + (int64_t)strip * g.nslices * 8 * NB;
 #pragma unroll
     for (int i = 0; i < OPT; ++i)
-        __hip_atomic_store(slots + (int64_t)s * 8 * NB + tid + THREADS * i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((tid + THREADS * i) / NB < d.M)
+            __hip_atomic_store(slots + (int64_t)s * 8 * NB + tid + THREADS * i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads(); // every partial store of this workgroup has completed (s_waitcnt before s_barrier)
     if (tid == 0)
         last_flag = __hip_atomic_fetch_add(g.cnt + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g.nslices - 1;
