@@ -11,7 +11,8 @@ widened by the activation's slope (at most 1; the float exp/tanh add a few ulp):
 
 Every kernel family the router can pick is covered: the fp32 MFMA kernel, the 16-bit direct-load
 kernel (bf16, half output and fp32 output), the small-K persistent kernel (fp16, K = 128, >= 1024
-tiles) and the GEMV (M = 1 and M = 8), with per-column, full and batch-broadcast bias.
+tiles) and both GEMV kernels (matrix-core: bf16 at M = 1 and 8; dot-product: fp32, and bf16
+narrower than 64 columns), with per-column, full and batch-broadcast bias.
 """
 import ctypes
 
@@ -125,6 +126,13 @@ def test_fp16_small_k_persistent(act, bias_kind):
 @pytest.mark.parametrize("act", list(ACTS), ids=lambda a: ACT_NAMES[a])
 def test_gemv(M, act):
     run_case(tv.BFLOAT16, tv.BFLOAT16, 0, M, 2048, 1104, "col", act, seed=4 + M)
+
+
+@pytest.mark.parametrize("act", [tv.ACT_SILU, tv.ACT_SIGMOID])
+def test_gemv_narrow_bf16(act):
+    """16-bit W narrower than 64 columns runs on the dot-product GEMV kernel (wider W on the
+    matrix-core kernel, test_gemv above)."""
+    run_case(tv.BFLOAT16, tv.BFLOAT16, 0, 3, 512, 40, "full", act, seed=14)
 
 
 @pytest.mark.parametrize("act", [tv.ACT_RELU, tv.ACT_TANH])
