@@ -123,8 +123,9 @@ typedef struct tv_epilogue {
  * enum tv_act return TV_E_UNSUPPORTED. */
 int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_stream);
 
-/* Skinny-M (M <= 8) matrix-vector path: HBM-streaming, no matrix cores.  Returns
- * TV_E_UNSUPPORTED for M > 8 or for a dtype pair it does not serve. */
+/* Skinny-M (M <= 8) matrix-vector path, HBM-streaming: matrix cores for bf16/fp16 W of 64 or more
+ * columns, packed dot products otherwise.  Returns TV_E_UNSUPPORTED for M > 8 or for a dtype pair
+ * or layout it does not serve. */
 int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream);
 
 /* Strided -> contiguous copy of one tensor view on the device (ndim <= TV_MAX_DIMS).  Element
