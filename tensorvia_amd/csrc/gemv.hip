@@ -19,8 +19,8 @@
 //  * x's slice is staged in LDS once per workgroup (while the first W loads are in flight);
 //  * products use the packed dot instructions over row pairs / quads of W, with the pairs built by
 //    v_perm_b32: v_dot2_f32_bf16 / v_dot2_f32_f16 (fp32 accumulation), v_dot4_i32_i8 (exact int32
-//    accumulation); fp32 uses fp32 FMA.  16-bit W with N >= 64 goes to gemv_mfma_kernel instead
-//    (matrix cores, W transposed through LDS), which is VALU-light and faster at every M;
+//    accumulation); fp32 uses fp32 FMA.  16-bit W with N >= 64, and int8 W with N >= 128 at
+//    M >= 3, go to gemv_mfma_kernel instead (matrix cores, W transposed through LDS);
 //  * the k-lanes are summed through LDS in a fixed order;
 //  * with S > 1 each workgroup publishes its strip partial to slot s (agent-coherent stores) and
 //    counts itself in with an agent-scope atomic; the workgroup that arrives last sums slots
@@ -305,10 +305,11 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
     if (tid == 0) __hip_atomic_store(g.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Matrix-core variant for 16-bit W (the dot-product loop above is VALU-bound at larger M: 16 v_dot2
-// per x row per 64 bytes of W).  Same strips (64 columns, 128 bytes of each W row), K slices and
-// slot combine; inside a workgroup, the WAVES waves take 32-row chunks of the slice in turn (chunk
-// c goes to wave c mod WAVES):
+// Matrix-core variant for 16-bit and int8 W (the dot-product loop above is VALU-bound at larger M:
+// 16 v_dot2 or v_dot4 per x row per 64 bytes of W).  Described here for 16 bits; int8 has 128-column
+// strips, 64-row chunks, v_mfma_i32_16x16x64_i8, ds_read_b64_tr_b8 and exact int32 sums.  Same
+// strips (128 bytes of each W row), K slices and slot combine; inside a workgroup, the WAVES waves
+// take 32-row chunks of the slice in turn (chunk c goes to wave c mod WAVES):
 //  * a chunk is 4 KB: 4 nontemporal 16-byte buffer loads per lane (lane l: rows l/8 + 8q, columns
 //    8 (l mod 8) ..), DEPTH chunks in flight per wave;
 //  * the wave writes it to its own LDS tile (32 rows x 64 columns, row pitch 144 bytes) and reads it
@@ -320,17 +321,25 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
 // A wave's LDS tile is private to it: LDS instructions of one wave execute in order, so the next
 // chunk's stores cannot overtake the previous chunk's reads.
 constexpr int kGemvMfmaPitch = 144;
-constexpr int kGemvMfmaWaves = 4, kGemvMfmaDepth = 2; // best of 2/4/8 waves x 1-8 chunks on c5's W
+// 4 waves with 8 KB of loads in flight each (2 chunks at 16 bits, 1 at 8): the best of 2/4/8 waves
+// x 1-8 chunks on c5's W, and of 4/8 waves x 1-2 chunks on the same shape in int8.
+constexpr int kGemvMfmaWaves = 4;
+template <typename T> constexpr int gemv_mfma_depth() { return sizeof(T) == 2 ? 2 : 1; }
 
 template <typename T, int WAVES, int DEPTH>
 __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
-    constexpr int ES = 2, VEC = 8, NB = 64, CH = 32, PITCH = kGemvMfmaPitch, THREADS = WAVES * 64;
+    using Acc = typename GemvTraits<T>::Acc;
+    // 16-bit: 64-column strips, 32-row chunks (v_mfma_f32_16x16x32, ds_read_b64_tr_b16); int8:
+    // 128-column strips, 64-row chunks (v_mfma_i32_16x16x64_i8, ds_read_b64_tr_b8).
+    constexpr int ES = sizeof(T), VEC = 16 / ES, NB = 8 * VEC, CH = 64 / ES, NQ = CH / 8, NF = NB / 16;
+    constexpr int PITCH = kGemvMfmaPitch, THREADS = WAVES * 64;
+    static_assert(ES == 1 || ES == 2, "16-bit or 8-bit W");
     static_assert(8 * NB % THREADS == 0, "outputs per thread");
     const GemmDesc& d = g.d;
 
     extern __shared__ __attribute__((aligned(16))) char xs[]; // 8 rows x kpad x ES (launch size)
     __shared__ __attribute__((aligned(16))) char wt[WAVES][CH * PITCH];
-    __shared__ float red[WAVES][8][NB];
+    __shared__ Acc red[WAVES][8][NB];
     __shared__ int last_flag;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -352,11 +361,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
     const bool col_ok = col < d.N; // N % VEC == 0 is a launch precondition
     const unsigned colb = (unsigned)(col * ES);
 
-    u32x4 w[DEPTH][4];
+    u32x4 w[DEPTH][NQ];
     auto issue = [&](int slot, int j) {
         const int c = wave + WAVES * j;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < NQ; ++q) {
             const int r = c * CH + r0 + 8 * q;
             const bool ok = col_ok && j < niter && r < ks; // rows past the slice read as zeros
             w[slot][q] = buf_load16_nt(wr, ok ? (unsigned)(r * rowb) + colb : kOOB);
@@ -378,14 +387,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
     }
     __syncthreads();
 
-    f32x4 acc[4];
+    typename Mfma<T>::Acc acc[NF];
 #pragma unroll
-    for (int f = 0; f < 4; ++f) acc[f] = f32x4{0, 0, 0, 0};
+    for (int f = 0; f < NF; ++f) acc[f] = typename Mfma<T>::Acc{0, 0, 0, 0};
     char* wl = wt[wave];
     const int wr_off = r0 * PITCH + cc * 16;
-    const int rd_off = (8 * (lane >> 4) + ((lane & 15) >> 2)) * PITCH + 8 * (lane & 3);
-    const bool arow = (lane & 15) < 8;
-    const char* xa = xs + (lane & 7) * kpad * ES + (lane >> 4) * 8 * ES;
+    // transpose reads: 16-bit, lanes 4r + c of a 16-lane group read row kb + r, columns 4c .. 4c + 3
+    // (then rows + 4); 8-bit, lanes 2r + c read row kb + r, columns 8c .. 8c + 7 (then rows + 8)
+    const int fr = lane & 15, kb = (lane >> 4) * (CH / 4);
+    const int rd_off = ES == 2 ? (kb + (fr >> 2)) * PITCH + 8 * (fr & 3) : (kb + (fr >> 1)) * PITCH + 8 * (fr & 1);
+    const bool arow = fr < 8;
+    const char* xa = xs + (lane & 7) * kpad * ES + kb * ES;
     for (int j0 = 0; j0 < niter; j0 += DEPTH) {
 #pragma unroll
         for (int dd = 0; dd < DEPTH; ++dd) {
@@ -393,16 +405,24 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
             if (j < niter) {
                 const int c = wave + WAVES * j;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(wl + wr_off + q * 8 * PITCH) = w[dd][q];
+                for (int q = 0; q < NQ; ++q) *reinterpret_cast<u32x4*>(wl + wr_off + q * 8 * PITCH) = w[dd][q];
                 u32x4 a = *reinterpret_cast<const u32x4*>(xa + c * CH * ES);
                 if (!arow) a = u32x4{0, 0, 0, 0};
 #pragma unroll
-                for (int f = 0; f < 4; ++f) {
+                for (int f = 0; f < NF; ++f) {
                     const lds_char* p = (const lds_char*)(wl + rd_off + f * 16 * ES);
-                    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
-                    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * PITCH));
-                    const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
-                    Mfma<T>::run(a, u32x4{l2.x, l2.y, h2.x, h2.y}, acc[f]);
+                    u32x4 bf;
+                    if constexpr (ES == 2) {
+                        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
+                        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * PITCH));
+                        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+                        bf = u32x4{l2.x, l2.y, h2.x, h2.y};
+                    } else {
+                        const i32x2_t lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
+                        const i32x2_t hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(p + 8 * PITCH));
+                        bf = u32x4{(unsigned)lo.x, (unsigned)lo.y, (unsigned)hi.x, (unsigned)hi.y};
+                    }
+                    Mfma<T>::run(a, bf, acc[f]);
                 }
                 if (j + DEPTH < niter) issue(dd, j + DEPTH);
             }
@@ -412,16 +432,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
     // Wave partials D[m][n] (m < 8: lanes 0..31) to red, then sum the waves in order.
     if (lane < 32)
 #pragma unroll
-        for (int f = 0; f < 4; ++f)
+        for (int f = 0; f < NF; ++f)
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[wave][4 * (lane >> 4) + r][16 * f + (lane & 15)] = acc[f][r];
     __syncthreads();
     constexpr int OPT = 8 * NB / THREADS; // outputs per thread
-    float v[OPT];
+    Acc v[OPT];
 #pragma unroll
     for (int i = 0; i < OPT; ++i) {
         const int o = tid + THREADS * i, m = o / NB, c = o % NB;
-        float t = red[0][m][c];
+        Acc t = red[0][m][c];
 #pragma unroll
         for (int wv = 1; wv < WAVES; ++wv) t += red[wv][m][c];
         v[i] = t;
@@ -442,7 +462,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
     // Publish slot s of this strip ([8][NB] floats, rows < M), count in; the last arriver sums the
     // slots in order.
     const int strip = lin;
-    float* slots = static_cast<float*>(g.part) + (int64_t)strip * g.nslices * 8 * NB;
+    Acc* slots = static_cast<Acc*>(g.part) + (int64_t)strip * g.nslices * 8 * NB;
 #pragma unroll
     for (int i = 0; i < OPT; ++i)
         if ((tid + THREADS * i) / NB < d.M)
@@ -456,12 +476,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
     for (int i = 0; i < OPT; ++i) {
         const int o = tid + THREADS * i, m = o / NB, c = o % NB;
         if (m < d.M && n0 + c < d.N) {
-            float part_v[kGemvMaxSlices];
+            Acc part_v[kGemvMaxSlices];
 #pragma unroll
             for (int k = 0; k < kGemvMaxSlices; ++k)
                 part_v[k] = k < g.nslices ? __hip_atomic_load(slots + (int64_t)k * 8 * NB + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                          : 0.0f;
-            float t = part_v[0];
+                                          : Acc(0);
+            Acc t = part_v[0];
 #pragma unroll
             for (int k = 1; k < kGemvMaxSlices; ++k)
                 if (k < g.nslices) t += part_v[k];
@@ -610,10 +630,19 @@ static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices) {
     return hipGetLastError();
 }
 
-// The matrix-core GEMV (bf16 / fp16, 64-column strips): same K-slice rule as gemv_run.
-template <typename T, int WAVES = kGemvMfmaWaves, int DEPTH = kGemvMfmaDepth>
+// The matrix-core GEMV (bf16 / fp16 with 64-column strips, int8 with 128-column strips): same
+// K-slice rule as gemv_run.
+template <typename T, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
 static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices) {
-    constexpr int NB = 64, VEC = 8, ES = 2, KCAP = gemv_kcap<T>();
+    using Acc = typename GemvTraits<T>::Acc;
+    constexpr int ES = sizeof(T), VEC = 16 / ES, NB = 8 * VEC, CH = 64 / ES;
+    // A workgroup's LDS (at most 160 KB) holds the kernel's static arrays and x's rows of a slice:
+    // x rows per slice are capped by both gemv_kcap and what the static arrays leave.
+    constexpr int kLds = 160 * 1024;
+    constexpr int kStatic = WAVES * CH * kGemvMfmaPitch + WAVES * 8 * NB * (int)sizeof(Acc) + 16;
+    static_assert(kStatic + 8 * ES * CH <= kLds, "static LDS leaves no room for x");
+    constexpr int kFit = (kLds - kStatic) / (8 * ES) / CH * CH;
+    constexpr int KCAP = gemv_kcap<T>() < kFit ? gemv_kcap<T>() : kFit; // a multiple of CH
     if (d.K < 1) return TV_E_UNSUPPORTED;
     const int nblk = (d.N + NB - 1) / NB;
     int S = nslices < 1 ? 1 : nslices;
@@ -639,11 +668,11 @@ static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices) {
         void* cnt = nullptr;
         int rc = get_workspace(stream, (size_t)nwg * sizeof(int), &cnt, 1);
         if (rc) return rc;
-        rc = get_workspace(stream, (size_t)nwg * S * 8 * NB * sizeof(float), &g.part, 2);
+        rc = get_workspace(stream, (size_t)nwg * S * 8 * NB * sizeof(Acc), &g.part, 2);
         if (rc) return rc;
         g.cnt = static_cast<int*>(cnt);
     }
-    const int kpad = (kslice + 31) / 32 * 32; // at most KCAP, a multiple of 32
+    const int kpad = (kslice + CH - 1) / CH * CH; // at most KCAP, a multiple of CH
     hipLaunchKernelGGL((gemv_mfma_kernel<T, WAVES, DEPTH>), dim3((unsigned)nwg, S), dim3(WAVES * 64), (size_t)8 * kpad * ES, stream, g);
     return hipGetLastError();
 }
@@ -686,25 +715,33 @@ int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads,
     }
 }
 
-// The matrix-core kernel serves 16-bit W with whole 128-byte strips (N >= 64).  On c5's W (bf16
-// [4096, 11008]) it takes 18.7 / 19.3 / 20.2 us at M = 1 / 4 / 8 against the dot-product kernel's
-// 19.2 / 20.9 / 25.7 us.  Its slices: about 688 workgroups in all (172 strips x 4 measured best
-// among 1-12 slices), at least what x's LDS slice needs, and no more than leaves each wave two
-// 32-row chunks per slice.
+// The matrix-core kernel serves 16-bit W at every M and int8 W at M >= 3, with whole 128-byte
+// strips (N >= 64 columns at 16 bits, N >= 128 at 8).  On c5's W shape, against the dot-product
+// kernel: bf16 18.7 / 19.3 / 20.2 us at M = 1 / 4 / 8 (dot 19.2 / 20.9 / 25.7); int8 13.7 us at
+// M = 8 (dot 20.5) but 12.1 us at M = 1 (dot 11.5).  Its slices: about 128 KB of W per workgroup
+// (688 workgroups in all at 16 bits, 344 in int8: 4 slices of c5's K, best among 1-16), at least
+// what x's LDS slice needs, and no more than leaves each wave two chunks per slice.
 static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream) {
-    const int64_t strips = (int64_t)(d.N + 63) / 64 * d.batch;
-    const int max_s = d.K / 256 > 1 ? d.K / 256 : 1;
-    int s = (int)((688 + strips - 1) / strips);
+    const int es = (int)dtype_size(d.dtype_a);
+    const int nb = 128 / es, ch = 64 / es;
+    const int64_t strips = (int64_t)(d.N + nb - 1) / nb * d.batch;
+    const int max_s = d.K / (8 * ch) > 1 ? d.K / (8 * ch) : 1;
+    const int64_t target = es == 2 ? 688 : 344;
+    int s = (int)((target + strips - 1) / strips);
     if (s > max_s) s = max_s;
     if (s > kGemvMaxSlices) s = kGemvMaxSlices;
     // gemv_mfma_run raises s to what x's LDS slice needs
-    return d.dtype_a == TV_BFLOAT16 ? gemv_mfma_run<__bf16>(d, stream, s) : gemv_mfma_run<_Float16>(d, stream, s);
+    switch (d.dtype_a) {
+        case TV_BFLOAT16: return gemv_mfma_run<__bf16>(d, stream, s);
+        case TV_FLOAT16: return gemv_mfma_run<_Float16>(d, stream, s);
+        default: return gemv_mfma_run<int8_t>(d, stream, s);
+    }
 }
 
 int launch_gemv(const GemmDesc& d, hipStream_t stream) {
     if (!gemv_layout_ok(d)) return TV_E_UNSUPPORTED;
     if (d.N == 0 || d.batch == 0) return 0;
-    if ((d.dtype_a == TV_BFLOAT16 || d.dtype_a == TV_FLOAT16) && gemv_nl(d) == 8)
+    if ((d.dtype_a == TV_BFLOAT16 || d.dtype_a == TV_FLOAT16 || (d.dtype_a == TV_INT8 && d.M >= 3)) && gemv_nl(d) == 8)
         return launch_gemv_mfma(d, stream);
     const GemvPlan p = gemv_plan(d);
     return launch_gemv_plan(d, stream, p.nl, p.threads, p.nslices);
