@@ -124,7 +124,7 @@ typedef struct tv_epilogue {
 int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_stream);
 
 /* Skinny-M (M <= 8) matrix-vector path, HBM-streaming: matrix cores for bf16/fp16 W of 64 or more
- * columns, packed dot products otherwise.  Returns TV_E_UNSUPPORTED for M > 8 or for a dtype pair
+ * columns and int8 W of 128 or more columns at M >= 3, packed dot products otherwise.  Returns TV_E_UNSUPPORTED for M > 8 or for a dtype pair
  * or layout it does not serve. */
 int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream);
 
