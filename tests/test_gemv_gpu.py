@@ -83,6 +83,21 @@ def test_gemv_batched_and_broadcast(hip, M, N):
     np.testing.assert_array_equal(c3, rng.f32_to_bf16_bits(ref3))
 
 
+def test_gemv_int8_batched_and_broadcast_matrix_core(hip):
+    """int8 at M >= 3 with N >= 128 runs on the matrix-core kernel: per-batch and broadcast W,
+    int8 (low byte) and int32 outputs, bit-exact."""
+    Bt, M, K, N = 3, 4, 1088, 272
+    x = rng.uniform_int(46, Bt * M * K, -128, 127).astype(np.int8).reshape(Bt, M, K)
+    w3 = rng.uniform_int(47, Bt * K * N, -128, 127).astype(np.int8).reshape(Bt, K, N)
+    for w in (w3, w3[1]):
+        c = hip.gemv(to_torch(x, INT8), to_torch(np.ascontiguousarray(w), INT8))
+        c32 = hip.gemv(to_torch(x, INT8), to_torch(np.ascontiguousarray(w), INT8), out_dtype=INT32)
+        torch.cuda.synchronize()
+        exact = np.stack([orc.exact_int(x[i], w[i] if w.ndim == 3 else w) for i in range(Bt)])
+        np.testing.assert_array_equal(to_storage(c32), exact.astype(np.int32))
+        np.testing.assert_array_equal(to_storage(c), exact.astype(np.int8))
+
+
 def test_gemv_unsupported_layouts_report_and_gemm_serves_them(hip):
     K, N = 256, 64
     x = rng.uniform_int(44, K, -2, 2).astype(np.float32).reshape(1, K)
