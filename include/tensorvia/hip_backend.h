@@ -95,6 +95,15 @@ template <> struct MulBiasActImpl<via::Device::HIP> {
     static Tensor execute(const Tensor& a, const Tensor& b, const Tensor* bias, Activation act);
 };
 
+template <via::Device D> struct TransposeImpl;
+// Materialising permutation on the device (tv_hip_repack; replaces TransposeImpl<Device::CUDA>,
+// src/backend/cuda/transpose.cu:129-174).  The dst overload reshapes dst to the permuted shape and
+// writes into its storage, as the reference's does.
+template <> struct TransposeImpl<via::Device::HIP> {
+    static Tensor execute(const Tensor& a, std::initializer_list<int64_t> axes);
+    static void execute(const Tensor& a, Tensor& dst, std::initializer_list<int64_t> axes);
+};
+
 template <via::Device D> struct TypecastImpl;
 template <via::Device D> struct FillImpl;
 template <via::Device D> struct RandomImpl;

@@ -29,6 +29,10 @@ OPS_API Tensor MulBiasAct(const Tensor& a, const Tensor& b, const Tensor* bias, 
 
 // Materialising N-d transpose (reference src/ops.cpp:1380-1402).
 OPS_API Tensor Transpose(const Tensor& a, std::initializer_list<int64_t> axes);
+// Into an existing tensor (reference include/core/ops.h:105, src/ops.cpp:1354-1378): dst must hold
+// as many elements as a; it is reshaped to the permuted shape and overwritten.  HIP tensors, dst of
+// a's dtype and not sharing a's storage.
+OPS_API void Transpose(const Tensor& a, Tensor& dst, std::initializer_list<int64_t> axes);
 OPS_API void Transpose(Tensor& a); // 2-d, in place
 // Zero-copy spelling used by the reference README (README.md:137): the permuted view.
 OPS_API Tensor transpose(const Tensor& a, std::initializer_list<int64_t> axes);

@@ -85,6 +85,7 @@ int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
 // Routing shared by tv_hip_gemm and tv_hip_gemm_ex.
 int run_gemm(const tv_gemm_args* args, const tvk::GemmDesc& d, hipStream_t s) {
     if (d.batch == 0 || d.M == 0 || d.N == 0) return TV_OK;
+    if (mfma_pair(args) && d.K == 0) return tvk::launch_gemm_k0(d, s);
     if (mfma_pair(args)) {
         if (d.M <= 8) {
             const int rc = tvk::launch_gemv(d, s);
@@ -153,6 +154,7 @@ int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream) {
     if (d.M > 8) return TV_E_UNSUPPORTED;
     if (!mfma_pair(args)) return TV_E_UNSUPPORTED;
     if (d.batch == 0 || d.M == 0 || d.N == 0) return TV_OK;
+    if (d.K == 0) return tvk::launch_gemm_k0(d, static_cast<hipStream_t>(hip_stream));
     return tvk::launch_gemv(d, static_cast<hipStream_t>(hip_stream));
 }
 

@@ -176,7 +176,34 @@ static int launch_t(const GemmDesc& d, hipStream_t stream) {
     }
 }
 
+// K = 0: every output is the empty sum, through the fused epilogue when one is given (act(bias)).
+__global__ __launch_bounds__(256) void gemm_k0_kernel(GemmDesc d) {
+    const int64_t total = (int64_t)d.batch * d.M * d.N;
+    for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t n = o % d.N;
+        const int64_t m = (o / d.N) % d.M;
+        const int64_t b = o / ((int64_t)d.N * d.M);
+        const float v = has_epilogue(d) ? epilogue_value(0.0f, d, b, m, n) : 0.0f;
+        const int64_t i = b * d.sc_b + m * d.sc_m + n * d.sc_n;
+        switch (d.dtype_c) {
+            case TV_BFLOAT16: static_cast<__bf16*>(d.C)[i] = static_cast<__bf16>(v); break;
+            case TV_FLOAT16: static_cast<_Float16*>(d.C)[i] = static_cast<_Float16>(v); break;
+            case TV_FLOAT32: static_cast<float*>(d.C)[i] = v; break;
+            default: store_as<int>(d.C, d.dtype_c, i, 0); break;
+        }
+    }
+}
+
 } // namespace simt
+
+int launch_gemm_k0(const GemmDesc& d, hipStream_t stream) {
+    const int64_t total = (int64_t)d.batch * d.M * d.N;
+    if (total == 0) return 0;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(simt::gemm_k0_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, d);
+    return hipGetLastError();
+}
 
 int launch_gemm_simt(const GemmDesc& d, hipStream_t stream) {
     if ((int64_t)d.batch * d.M * d.N == 0) return 0;

@@ -1,6 +1,8 @@
 // Skinny-M (M <= 8) matmul for decode-shaped calls: x[b, M, K] @ W[b, K, N], W row-major
-// (N-contiguous).  HBM-bound: W is streamed exactly once with 16-byte buffer loads and no matrix
-// cores.
+// (N-contiguous).  HBM-bound: W is streamed exactly once with 16-byte buffer loads.  Two kernels:
+// a packed-dot-product kernel (gemv_kernel, no matrix cores) and a matrix-core kernel
+// (gemv_mfma_kernel) that serves 16-bit W of 64 or more columns at every M and int8 W of 128 or
+// more columns at M >= 3, where the dot products would make the VALU, not HBM, the bound.
 //
 // The reference computes these shapes with mul_kernel_basic (src/backend/cpu/mul.cpp:7-25), chosen
 // because batch*M*N < 2^20 (mul.cpp:87-96), on one OpenMP thread when M = 1.
@@ -22,10 +24,11 @@
 //    accumulation); fp32 uses fp32 FMA.  16-bit W with N >= 64, and int8 W with N >= 128 at
 //    M >= 3, go to gemv_mfma_kernel instead (matrix cores, W transposed through LDS);
 //  * the k-lanes are summed through LDS in a fixed order;
-//  * with S > 1 each workgroup publishes its strip partial to slot s (agent-coherent stores) and
-//    counts itself in with an agent-scope atomic; the workgroup that arrives last sums slots
-//    0..S-1 in order (deterministic), writes C and resets the counter.  No workgroup waits for
-//    another, and there is no second kernel.
+//  * with S > 1 each workgroup publishes its strip partial to slot s (agent-scope atomic stores,
+//    waited for before the workgroup counts itself in with an agent-scope atomic, see
+//    publish_and_count); the workgroup that arrives last sums slots 0..S-1 in order
+//    (deterministic), writes C and resets the counter.  No workgroup waits for another, and there
+//    is no second kernel.
 #include "gemm_mfma_impl.h"
 #include "tv_kernels.h"
 
@@ -149,6 +152,30 @@ __device__ inline void gemv_store(void* C, int64_t idx, int dtype_c, Acc v) {
 // run on the same XCD and meet in its L2 (workgroups are dealt round-robin over the 8 XCDs).
 __device__ inline int xcd_remap(int bid, int nwg) {
     return (nwg & 7) == 0 ? (bid & 7) * (nwg >> 3) + (bid >> 3) : bid;
+}
+
+// Split-K hand-over between the workgroups of one strip.  Called by every thread after its
+// partial-slot stores, which are agent-scope atomic stores (global_store ... sc1: written through
+// the XCD's L2 to the agent's coherence point, never left dirty in an L2).
+//  * Each wave waits until its own slot stores are acknowledged (s_waitcnt vmcnt(0); for a store
+//    the count drops when the write is complete at the scope it was issued with).  The asm's
+//    memory clobber keeps the compiler from moving the stores below the wait.
+//  * After the barrier every slot store of the workgroup is complete; thread 0 then counts the
+//    workgroup in with an agent-scope atomic add, so a count that completes the strip is taken
+//    after every publisher's stores are complete.
+//  * The combining workgroup reads the slots with agent-scope atomic loads (sc1), which are
+//    served from the coherence point, issued after the count returned (through the barrier).
+// This is the ordering-only release that rocPRIM's look-back scan uses on this architecture for
+// data published through agent-scope atomics: a C++ release/acquire fence pair at agent scope
+// also writes back and invalidates the XCD's whole L2 (buffer_wbl2 sc1, buffer_inv sc1) once per
+// wave, which measured 104 us on c5 (x[1,4096] @ W[4096,11008] bf16) against 18.5 us with this
+// hand-over; there is no dirty non-atomic data here for those to write back.
+// *last is 1 in the workgroup that must combine the slots.
+__device__ inline void publish_and_count(int* cnt, int nslices, int* last) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) *last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nslices - 1;
+    __syncthreads();
 }
 
 template <typename T, int MR, int NL, int THREADS> struct GemvShape {
@@ -280,10 +307,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
 #pragma unroll
         for (int m = 0; m < MR; ++m)
             if (m < d.M) __hip_atomic_store(slots + ((int64_t)s * MR + m) * NB + oc, v[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads(); // every partial store of this workgroup has completed (s_waitcnt before s_barrier)
-    if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(g.cnt + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g.nslices - 1;
-    __syncthreads();
+    publish_and_count(g.cnt + strip, g.nslices, &last_flag);
     if (!last_flag) return;
     for (int o = tid; o < MR * NB; o += THREADS) {
         const int m = o / NB, c = o - m * NB;
@@ -459,18 +483,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
         return;
     }
 
-    // Publish slot s of this strip ([8][NB] floats, rows < M), count in; the last arriver sums the
-    // slots in order.
+    // Publish slot s of this strip ([8][NB] accumulators, fp32 or int32, rows < M), count in; the
+    // last arriver sums the slots in order.
     const int strip = lin;
     Acc* slots = static_cast<Acc*>(g.part) + (int64_t)strip * g.nslices * 8 * NB;
 #pragma unroll
     for (int i = 0; i < OPT; ++i)
         if ((tid + THREADS * i) / NB < d.M)
             __hip_atomic_store(slots + (int64_t)s * 8 * NB + tid + THREADS * i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads(); // every partial store of this workgroup has completed (s_waitcnt before s_barrier)
-    if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(g.cnt + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g.nslices - 1;
-    __syncthreads();
+    publish_and_count(g.cnt + strip, g.nslices, &last_flag);
     if (!last_flag) return;
 #pragma unroll
     for (int i = 0; i < OPT; ++i) {
@@ -536,8 +557,8 @@ static int get_workspace(hipStream_t stream, size_t need, void** out, int kind) 
         e = hipMalloc(&w.base, sz);
         if (e != hipSuccess) return TV_E_NOMEM;
         w.bytes = sz;
-        // The arrival counters must start at zero (each launch leaves them at zero again).  A fill
-        // kernel rather than a memset node, for callers that capture.
+        // The arrival counters must start at zero (each launch leaves them at zero again).  This
+        // workspace is not meant for stream capture: growing it synchronises the stream.
         hipLaunchKernelGGL(gemv_zero_kernel, dim3(256), dim3(256), 0, stream, static_cast<int*>(w.base),
                            (int64_t)(sz / sizeof(int)));
         e = hipGetLastError();
@@ -596,6 +617,7 @@ static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices) {
     using Sh = GemvShape<T, MR, NL, THREADS>;
     using Acc = typename GemvTraits<T>::Acc;
     const int vec = Sh::VEC;
+    if (d.K < 1) return TV_E_UNSUPPORTED; // K = 0 is served by the zero-sum kernel
     const int nblk = (d.N + Sh::NB - 1) / Sh::NB;
     int S = nslices < 1 ? 1 : nslices;
     const int min_s = (d.K + Sh::KCAP - 1) / Sh::KCAP;

@@ -101,6 +101,7 @@ enum LoadMode : int {
 // Launchers (return hipError_t, or a negative TV_E_* code).
 int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream);
 int launch_gemm_simt(const GemmDesc& d, hipStream_t stream);
+int launch_gemm_k0(const GemmDesc& d, hipStream_t stream); // K = 0: C = epilogue(0)
 int launch_repack(const tv_repack_args* a, hipStream_t stream);
 int launch_typecast(const void* src, int src_dt, void* dst, int dst_dt, int64_t n, hipStream_t stream);
 int launch_fill(void* dst, int dt, int64_t n, float value, hipStream_t stream);

@@ -418,6 +418,40 @@ Tensor TypecastImpl<Device::HIP>::execute(const Tensor& a, DataType dst_type) {
     return out;
 }
 
+// ---- TransposeImpl<HIP> --------------------------------------------------------------------------
+
+Tensor TransposeImpl<Device::HIP>::execute(const Tensor& a, std::initializer_list<int64_t> axes) {
+    return a.permute(std::vector<int64_t>(axes)).contiguous(); // clone_as_contiguous: tv_hip_repack
+}
+
+void TransposeImpl<Device::HIP>::execute(const Tensor& a, Tensor& dst, std::initializer_list<int64_t> axes) {
+    if (a.device() != Device::HIP || dst.device() != Device::HIP)
+        throw std::runtime_error("Transpose: a and dst must be HIP tensors");
+    if (a.dtype() != dst.dtype())
+        throw std::runtime_error("Transpose: dst dtype " + std::string(dtype_to_string(dst.dtype())) +
+                                 " differs from the input's " + std::string(dtype_to_string(a.dtype())));
+    const Tensor view = a.permute(std::vector<int64_t>(axes));
+    std::vector<int64_t> shape = view.shape();
+    dst.reshape(shape); // as the reference (src/backend/cuda/transpose.cu:129-134); dst is dense after it
+    if (view.dims() > TV_MAX_DIMS) throw std::runtime_error("Transpose: too many dimensions");
+    // A permutation written over its own source would read elements it has already overwritten.
+    if (dst.get_impl() == a.get_impl()) throw std::runtime_error("Transpose: dst shares storage with a");
+    const size_t es = calc_dtype_size(a.dtype());
+    tv_repack_args r{};
+    r.ndim = static_cast<int32_t>(view.dims());
+    r.elem_size = static_cast<int32_t>(es);
+    const std::vector<int64_t> st = view.strides();
+    for (int d = 0; d < r.ndim; ++d) {
+        r.shape[d] = shape[d];
+        r.strides[d] = st[d];
+    }
+    r.src = static_cast<const char*>(view.data()) + view.offset() * es;
+    r.dst = static_cast<char*>(dst.data()) + dst.offset() * es;
+    auto ctx = hip_ctx_of(dst.get_impl());
+    tv_check(tv_hip_repack(&r, ctx->stream()), "ops::Transpose");
+    ctx->wait();
+}
+
 Tensor FillImpl<Device::HIP>::execute(const std::vector<int64_t>& shape, DataType dtype, float value) {
     Tensor out(shape, dtype, Device::HIP);
     auto ctx = hip_ctx_of(out.get_impl());

@@ -10,21 +10,26 @@ using namespace via;
 
 namespace ops {
 
-// Validation restates the reference's (src/ops.cpp:540-556) with one extension: a rank-3 A may
-// multiply a rank-2 B (B broadcast over the batch), which the reference rejects.
+// Validation restates the reference's (src/ops.cpp:540-556), in its order and with its messages,
+// with one extension: a rank-3 A may multiply a rank-2 B (B broadcast over the batch), which the
+// reference rejects as a rank mismatch.
 namespace {
 void check_mul_operands(const Tensor& a, const Tensor& b) {
-    if (a.device() != b.device()) throw std::runtime_error("Tensors a and b device mismatch!");
+    if (a.device() != b.device()) throw std::runtime_error("Tensors a and b device mismatch!"); // :542-543
     const size_t ra = a.dims(), rb = b.dims();
-    if (ra != 2 && ra != 3) throw std::runtime_error("Tensors a and b dims must be 2 or 3,but got " + std::to_string(ra));
-    if (rb != ra && !(ra == 3 && rb == 2))
+    if (rb != ra && !(ra == 3 && rb == 2)) // :544-545
         throw std::runtime_error("Tensors a and b must have the same rank,but got " + std::to_string(ra) + " and " +
                                  std::to_string(rb));
-    if (ra == 3 && rb == 3 && a.shape(0) != b.shape(0))
-        throw std::runtime_error("Tensors a and b must have the same batch size");
-    if (a.shape(-1) != b.shape(-2))
-        throw std::runtime_error("Tensors common dim must match,but " + std::to_string(a.shape(-1)) + " and " +
-                                 std::to_string(b.shape(-2)));
+    if (ra != 2 && ra != 3) throw std::runtime_error("Tensors a and b dims must be 2 or 3,but got " + std::to_string(ra)); // :546-547
+    if (ra == 3) { // :548-552
+        if (rb == 3 && a.shape(0) != b.shape(0)) throw std::runtime_error("Tensors a and b must have the same batch size");
+        if (a.shape(2) != b.shape(-2))
+            throw std::runtime_error("Tensors common dim must match,but " + std::to_string(a.shape(2)) + " and " +
+                                     std::to_string(b.shape(-2)));
+    } else if (a.shape(1) != b.shape(0)) { // :553-556; the reference's message names dimension 0 of both
+        throw std::runtime_error("Tensors common dim must match,but " + std::to_string(a.shape(0)) + " and " +
+                                 std::to_string(b.shape(0)));
+    }
     if (a.device() == Device::CPU)
         throw std::runtime_error("ops::Mul on CPU tensors runs the reference CPU backend, which is not part of the "
                                  "HIP build; move both tensors with to_device()");
@@ -48,10 +53,23 @@ Tensor transpose(const Tensor& a, std::initializer_list<int64_t> axes) {
     return a.permute(std::vector<int64_t>(axes));
 }
 
+// Validation as the reference's (src/ops.cpp:1380-1385); device tensors are permuted on the device.
 Tensor Transpose(const Tensor& a, std::initializer_list<int64_t> axes) {
     if (a.dims() == 0) throw std::runtime_error("Input tensor must be not null.");
     if (a.dims() != axes.size()) throw std::runtime_error("transpose shape and axes size not match");
-    return a.permute(std::vector<int64_t>(axes)).contiguous();
+    if (a.device() == Device::HIP) return TransposeImpl<Device::HIP>::execute(a, axes);
+    return a.permute(std::vector<int64_t>(axes)).contiguous(); // host tensors: host gather
+}
+
+// Validation as the reference's (src/ops.cpp:1354-1361): dst is reshaped to the permuted shape and
+// receives the permuted elements.
+void Transpose(const Tensor& a, Tensor& dst, std::initializer_list<int64_t> axes) {
+    if (a.dims() == 0) throw std::runtime_error("Input tensor must be not null.");
+    if (a.dims() != axes.size()) throw std::runtime_error("transpose shape and axes size not match");
+    if (a.numel() != dst.numel()) throw std::runtime_error("dst numel not enough");
+    if (a.device() != Device::HIP)
+        throw std::runtime_error("ops::Transpose into dst runs on HIP tensors; move both with to_device()");
+    TransposeImpl<Device::HIP>::execute(a, dst, axes);
 }
 
 void Transpose(Tensor& a) {

@@ -63,16 +63,21 @@ def compute_type(a: int, b: int) -> int:
 
 
 def _check_shapes(a: torch.Tensor, b: torch.Tensor) -> None:
+    """The reference's checks in its order (src/ops.cpp:542-556), with the broadcast extension."""
     if a.device != b.device:
         raise RuntimeError("Tensors a and b device mismatch!")
+    if b.dim() != a.dim() and not (a.dim() == 3 and b.dim() == 2):
+        raise RuntimeError(f"Tensors a and b must have the same rank,but got {a.dim()} and {b.dim()}")
     if a.dim() not in (2, 3):
         raise RuntimeError(f"Tensors a and b dims must be 2 or 3,but got {a.dim()}")
-    if b.dim() not in (2, 3) or (a.dim() == 2 and b.dim() == 3):
-        raise RuntimeError(f"Tensors a and b must have the same rank,but got {a.dim()} and {b.dim()}")
-    if b.dim() == 3 and a.shape[0] != b.shape[0]:
-        raise RuntimeError("Tensors a and b must have the same batch size")
-    if a.shape[-1] != b.shape[-2]:
-        raise RuntimeError(f"Tensors common dim must match,but {a.shape[-1]} and {b.shape[-2]}")
+    if a.dim() == 3:
+        if b.dim() == 3 and a.shape[0] != b.shape[0]:
+            raise RuntimeError("Tensors a and b must have the same batch size")
+        if a.shape[2] != b.shape[-2]:
+            raise RuntimeError(f"Tensors common dim must match,but {a.shape[2]} and {b.shape[-2]}")
+    elif a.shape[1] != b.shape[0]:
+        # the reference's 2-d message names dimension 0 of both operands (src/ops.cpp:555)
+        raise RuntimeError(f"Tensors common dim must match,but {a.shape[0]} and {b.shape[0]}")
 
 
 def make_args(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor) -> TvGemmArgs:

@@ -133,10 +133,30 @@ int main(int argc, char** argv) {
         Tensor bad_k({6, 3}, DataType::FLOAT32, Device::CPU);
         Tensor a3({2, 4, 5}, DataType::FLOAT32, Device::CPU), b3({3, 5, 3}, DataType::FLOAT32, Device::CPU);
         Tensor a4({1, 2, 4, 5}, DataType::FLOAT32, Device::CPU);
-        expect_throw("mul_validation_messages", [&] { ops::Mul(a2, bad_k); }, "common dim must match");
-        expect_throw("mul_validation_messages", [&] { ops::Mul(a2, a3); }, "same rank");
-        expect_throw("mul_validation_messages", [&] { ops::Mul(a4, a4); }, "dims must be 2 or 3");
-        expect_throw("mul_validation_messages", [&] { ops::Mul(a3, b3); }, "same batch size");
+        Tensor bad_k3({2, 6, 3}, DataType::FLOAT32, Device::CPU);
+        // Messages and their order are the reference's (src/ops.cpp:542-556): the rank check comes
+        // before the 2-or-3 check, and the 2-d message names dimension 0 of both operands.
+        expect_throw("mul_validation_messages", [&] { ops::Mul(a2, bad_k); },
+                     "Tensors common dim must match,but 4 and 6");
+        expect_throw("mul_validation_messages", [&] { ops::Mul(a3, bad_k3); },
+                     "Tensors common dim must match,but 5 and 6");
+        expect_throw("mul_validation_messages", [&] { ops::Mul(a2, a3); },
+                     "Tensors a and b must have the same rank,but got 2 and 3");
+        expect_throw("mul_validation_messages", [&] { ops::Mul(a4, a2); },
+                     "Tensors a and b must have the same rank,but got 4 and 2");
+        expect_throw("mul_validation_messages", [&] { ops::Mul(a4, a4); }, "Tensors a and b dims must be 2 or 3,but got 4");
+        expect_throw("mul_validation_messages", [&] { ops::Mul(a3, b3); }, "Tensors a and b must have the same batch size");
+        expect_throw("mul_validation_messages", [&] { ops::Mul(a2, a4); }, "same rank");
+        // The broadcast extension: rank-3 A with rank-2 B passes validation (then needs the device).
+        expect_throw("mul_validation_messages", [&] { ops::Mul(a3, b2); }, "to_device");
+        // A zero-sized dimension is rejected when the tensor is built (type_traits.h:296), so K = 0
+        // never reaches ops::Mul.
+        expect_throw("mul_validation_messages", [&] { Tensor k0({4, 0}, DataType::FLOAT32, Device::CPU); },
+                     "Invalid tensor dimension");
+        Tensor dst({7}, DataType::FLOAT32, Device::CPU);
+        expect_throw("mul_validation_messages", [&] { ops::Transpose(a2, dst, {1, 0}); }, "dst numel not enough");
+        expect_throw("mul_validation_messages", [&] { ops::Transpose(a2, dst, {1, 0, 2}); },
+                     "transpose shape and axes size not match");
         // Valid shapes on CPU tensors: the CPU backend is not part of this build.
         expect_throw("mul_validation_messages", [&] { ops::Mul(a2, b2); }, "to_device");
     });

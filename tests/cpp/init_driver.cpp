@@ -13,7 +13,14 @@
 //                    &Random({80}, bf16, -2, 2, 92), act)          (B and the bias broadcast)
 //   fused_f32_full   ops::MulBiasAct(Random({64,96}, fp32, -1, 1, 93), Random({96,80}, fp32, -1, 1, 94),
 //                    &Random({64,80}, fp32, -2, 2, 95), Silu)
-//   "threw <name>" lines: calls that must throw (bias of the wrong dtype or shape).
+//   tdst_<i>         ops::Transpose(src, dst, axes) into a 1-d dst of the same element count
+//                    (dst reshaped to the permuted shape): i = 0..2 permute an int32
+//                    Random({4, 6, 10}, -1000, 999, seed 100) by {2,0,1}, {0,2,1}, {1,0,2};
+//                    i = 3 permutes fp16 Random({3, 40, 16}, -1, 1, seed 101) by {0,2,1} (config c4's
+//                    materialised K^T); i = 4 permutes the slice [1:3, 2:6, :] of the int32 source by
+//                    {2,1,0} (a view with an offset)
+//   "threw <name>" lines: calls that must throw (bias of the wrong dtype or shape; Transpose into a
+//   dst of another dtype or into a's own storage).
 #include <cstdio>
 #include <fstream>
 #include <string>
@@ -85,6 +92,30 @@ int main(int argc, char** argv) {
         return ops::MulBiasAct(ops::Random({64, 96}, DataType::FLOAT32, -1.0f, 1.0f, 93),
                                ops::Random({96, 80}, DataType::FLOAT32, -1.0f, 1.0f, 94), &bias, ops::Activation::Silu);
     });
+    const std::vector<std::vector<int64_t>> perms = {{2, 0, 1}, {0, 2, 1}, {1, 0, 2}};
+    for (int i = 0; i < 3; ++i)
+        run("tdst_" + std::to_string(i), [&] {
+            const Tensor src = ops::Random({4, 6, 10}, DataType::INT32, -1000.0f, 999.0f, 100);
+            Tensor dst = ops::Zeros({240}, DataType::INT32);
+            const auto& p = perms[i];
+            ops::Transpose(src, dst, {p[0], p[1], p[2]});
+            if (dst.dims() != 3 || dst.shape(0) != src.shape(p[0]) || dst.shape(2) != src.shape(p[2]))
+                throw std::runtime_error("dst not reshaped to the permuted shape");
+            return dst;
+        });
+    run("tdst_3", [&] {
+        const Tensor src = ops::Random({3, 40, 16}, DataType::FLOAT16, -1.0f, 1.0f, 101);
+        Tensor dst = ops::Zeros({1920}, DataType::FLOAT16);
+        ops::Transpose(src, dst, {0, 2, 1});
+        return dst;
+    });
+    run("tdst_4", [&] {
+        const Tensor src = ops::Random({4, 6, 10}, DataType::INT32, -1000.0f, 999.0f, 100);
+        const Tensor view = src.slice({{1, 3}, {2, 6}});
+        Tensor dst = ops::Zeros({80}, DataType::INT32);
+        ops::Transpose(view, dst, {2, 1, 0});
+        return dst;
+    });
     auto must_throw = [&](const std::string& name, auto&& f) {
         try {
             f();
@@ -103,6 +134,10 @@ int main(int argc, char** argv) {
     const Tensor ai = ops::Random({64, 96}, DataType::INT8, -3.0f, 3.0f, 5);
     const Tensor bi = ops::Random({96, 80}, DataType::INT8, -3.0f, 3.0f, 6);
     must_throw("int8_output", [&] { ops::MulBiasAct(ai, bi, nullptr, ops::Activation::Relu); });
+    Tensor tdst_f32 = ops::Zeros({64 * 96}, DataType::FLOAT32);
+    must_throw("transpose_dst_dtype", [&] { ops::Transpose(a, tdst_f32, {1, 0}); });
+    Tensor self = ops::Random({8, 8}, DataType::FLOAT32, -1.0f, 1.0f, 7);
+    must_throw("transpose_dst_self", [&] { ops::Transpose(self, self, {1, 0}); });
     std::printf("failures %d\n", failures);
     return failures ? 1 : 0;
 }

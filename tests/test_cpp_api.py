@@ -57,5 +57,8 @@ def test_libtensorvia_exports_the_plugin_api():
                 "ops::Mul(Tensor const&, Tensor const&)", "ops::matmul(Tensor const&, Tensor const&)",
                 "HIPContext::get()", "HIPTensor::clone_as_contiguous(Metadata const&) const",
                 "register_tensor_impl(", "copy_device_to_host(", "copy_host_to_device(",
-                "ops::Transpose(Tensor const&, std::initializer_list<long>)", "ops::Typecast(Tensor const&, via::DataType)"]:
+                "ops::Transpose(Tensor const&, std::initializer_list<long>)",
+                "ops::Transpose(Tensor const&, Tensor&, std::initializer_list<long>)",
+                "ops::TransposeImpl<(via::Device)4>::execute(Tensor const&, Tensor&, std::initializer_list<long>)",
+                "ops::Typecast(Tensor const&, via::DataType)"]:
         assert sym in names, sym

@@ -38,6 +38,9 @@ CASES = [
     ("i32_simt", INT32, INT32, "contig", 0, 50, 70, 40, -50, 50, 23, 24),
     ("i32_f32_mixed", INT32, FLOAT32, "contig", 0, 33, 65, 17, -50, 50, 25, 26),
 ]
+# K = 0 cannot reach ops::Mul: a tensor with a zero-sized dimension is rejected when it is built
+# (calc_numel, reference include/core/type_traits.h:296; tests/cpp/host_api_test.cpp checks it).
+# The C-ABI serves K = 0 (tests/test_edge_gpu.py).
 
 
 def _base_shapes(layout, batch, M, K, N):

@@ -138,6 +138,31 @@ def test_cpp_mul_bias_act_fp32_full_bias_and_errors(init_run):
         assert re.search(rf"^threw {name}: ", r.stdout, re.M), r.stdout[-2000:]
 
 
+@pytest.mark.parametrize("i", range(5))
+def test_cpp_transpose_into_dst(init_run, i):
+    """ops::Transpose(a, dst, axes) (reference src/ops.cpp:1354-1378): dst, a 1-d tensor of the same
+    element count, is reshaped to the permuted shape and holds numpy's transpose, bit for bit."""
+    r, out, done = init_run
+    assert f"tdst_{i}" in done, r.stdout[-2000:]
+    src = rng.make("uniform", (4, 6, 10), 100, "int32", -1000, 999)
+    if i < 3:
+        want = np.transpose(src, [(2, 0, 1), (0, 2, 1), (1, 0, 2)][i])
+        dt = INT32
+    elif i == 3:
+        want = np.transpose(rng.make("uniform", (3, 40, 16), 101, "float16", -1, 1), (0, 2, 1))
+        dt = FLOAT16
+    else:
+        want = np.transpose(src[1:3, 2:6, :], (2, 1, 0))
+        dt = INT32
+    np.testing.assert_array_equal(_read(out, f"tdst_{i}", dt, want.shape), np.ascontiguousarray(want))
+
+
+def test_cpp_transpose_into_dst_errors(init_run):
+    r, _, _ = init_run
+    for name in ("transpose_dst_dtype", "transpose_dst_self"):
+        assert re.search(rf"^threw {name}: ", r.stdout, re.M), r.stdout[-2000:]
+
+
 def test_cpp_init_driver_exit_status(init_run):
     r, _, _ = init_run
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]

@@ -152,10 +152,12 @@ def test_half_uniform_vs_oracle(hip, dt):
     assert_half_close(c, ref, orc.abs_bound(to_f32(x, dt), to_f32(y, dt)), K)
 
 
-def test_bf16_config3_broadcast_equals_flattened(hip):
-    """c3 at reduced batch: A[4,2048,4096] @ B[4096,4096] (B broadcast, batch stride 0) equals the
-    flattened call [4*2048,4096] @ [4096,4096] bit for bit, and sampled rows match the oracle."""
-    Bt, M, K, N = 4, 2048, 4096, 4096
+def test_bf16_config3_full_size_broadcast_equals_flattened(hip):
+    """c3 at its configured size: A[16,2048,4096] @ B[4096,4096] (B broadcast, batch stride 0; 2,048
+    output tiles) equals the flattened call [32768,4096] @ [4096,4096] bit for bit (the reference
+    rejects the broadcast form, so the flattened 2-d call is what it computes, mul.cpp:97-145), and
+    48 sampled rows, 3 in each of the 16 batches, match the oracle under the bf16 bar."""
+    Bt, M, K, N = 16, 2048, 4096, 4096
     a = rng.make("uniform", (Bt, M, K), 5, "bfloat16")
     b = rng.make("uniform", (K, N), 6, "bfloat16")
     ta, tb = to_torch(a, BFLOAT16), to_torch(b, BFLOAT16)
@@ -163,11 +165,13 @@ def test_bf16_config3_broadcast_equals_flattened(hip):
     c2 = hip.gemm(ta.reshape(Bt * M, K), tb)
     torch.cuda.synchronize()
     assert torch.equal(c3.reshape(Bt * M, N), c2)
-    c = to_f32(to_storage(c3), BFLOAT16).reshape(Bt * M, N)
-    rows = np.random.default_rng(2).choice(Bt * M, 32, replace=False)
+    r = np.random.default_rng(2)
+    rows = np.concatenate([bi * M + r.choice(M, 3, replace=False) for bi in range(Bt)])
+    c = to_f32(to_storage(c3.reshape(Bt * M, N)[torch.from_numpy(rows).cuda()]), BFLOAT16)
+    del c3, c2, ta
     xa = a.reshape(Bt * M, K)[rows]
     ref = orc.mul(xa, BFLOAT16, b, BFLOAT16)
-    assert_half_close(c[rows], ref, orc.abs_bound(to_f32(xa, BFLOAT16), to_f32(b, BFLOAT16)), K)
+    assert_half_close(c, ref, orc.abs_bound(to_f32(xa, BFLOAT16), to_f32(b, BFLOAT16)), K)
 
 
 def test_fp16_config4_transposed_view(hip):
