@@ -79,7 +79,8 @@ enum tv_status {
     TV_E_DTYPE = -3,       /* dtype value out of range or output dtype not allowed for the inputs */
     TV_E_UNSUPPORTED = -4, /* valid request that this entry point does not serve (e.g. gemv with M > 8) */
     TV_E_INJECTED = -5,    /* returned by the fault-injection hook (tests only) */
-    TV_E_NOMEM = -6        /* workspace allocation failed */
+    TV_E_NOMEM = -6,       /* workspace allocation failed */
+    TV_E_SCRATCH = -7      /* tv_hip_gemm_noalloc: the call needs more split-K scratch than the static buffer holds */
 };
 
 typedef struct tv_gemm_args {
@@ -122,6 +123,18 @@ typedef struct tv_epilogue {
  * (sc_n = 1; any C layout when M <= 8); integer outputs, a column-strided C and an act outside
  * enum tv_act return TV_E_UNSUPPORTED. */
 int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_stream);
+
+/* tv_hip_gemm that allocates nothing.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, routing, kernels and results as tv_hip_gemm; the one scratch
+ * buffer tv_hip_gemm allocates, the split-K partials of the M <= 8 GEMV kernels, comes instead from
+ * a static device array of 4 MiB of partial slots plus 16,384 arrival counters per GPU, held until
+ * the process ends.  A call whose split needs more returns TV_E_SCRATCH (e.g. M = 8 bf16 needs
+ * 2 KiB per (64-column strip, K-slice) pair: c5's x[8,4096] @ W[4096,11008] needs 1.4 MiB).
+ * The first call on a GPU looks the array up (hipGetSymbolAddress) and clears its counters with a
+ * kernel on hip_stream.  All calls on one GPU share its array: calls that overlap on one GPU (on
+ * different streams, or from different threads) race and must be serialised by the caller. */
+int tv_hip_gemm_noalloc(const tv_gemm_args* args, void* hip_stream);
 
 /* Skinny-M (M <= 8) matrix-vector path, HBM-streaming: matrix cores for bf16/fp16 W of 64 or more
  * columns and int8 W of 128 or more columns at M >= 3, packed dot products otherwise.  Returns TV_E_UNSUPPORTED for M > 8 or for a dtype pair
@@ -172,7 +185,7 @@ int tv_hip_abi_version(void);
  * the device.  Lets host code prove error propagation without a GPU.  count = 0 disarms. */
 void tv_hip_inject_fault(int code, int count);
 
-#define TV_HIP_ABI_VERSION 4
+#define TV_HIP_ABI_VERSION 5
 
 #ifdef __cplusplus
 }

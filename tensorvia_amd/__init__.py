@@ -24,10 +24,10 @@ DTYPE_NAMES = {INT8: "int8", INT16: "int16", INT32: "int32", INT64: "int64",
                BFLOAT16: "bfloat16", FLOAT16: "float16", FLOAT32: "float32", FLOAT64: "float64"}
 
 TV_OK = 0
-TV_E_NULL, TV_E_SHAPE, TV_E_DTYPE, TV_E_UNSUPPORTED, TV_E_INJECTED, TV_E_NOMEM = -1, -2, -3, -4, -5, -6
+TV_E_NULL, TV_E_SHAPE, TV_E_DTYPE, TV_E_UNSUPPORTED, TV_E_INJECTED, TV_E_NOMEM, TV_E_SCRATCH = -1, -2, -3, -4, -5, -6, -7
 
 # Every symbol include/tensorvia_hip.h declares.
-EXPORTED_SYMBOLS = ("tv_hip_gemm", "tv_hip_gemm_ex", "tv_hip_gemv", "tv_hip_repack", "tv_hip_typecast", "tv_hip_fill",
+EXPORTED_SYMBOLS = ("tv_hip_gemm", "tv_hip_gemm_ex", "tv_hip_gemm_noalloc", "tv_hip_gemv", "tv_hip_repack", "tv_hip_typecast", "tv_hip_fill",
                     "tv_hip_random", "tv_hip_strerror", "tv_hip_abi_version", "tv_hip_inject_fault")
 
 
@@ -86,6 +86,8 @@ def lib() -> ctypes.CDLL:
         L.tv_hip_gemm.restype = ctypes.c_int
         L.tv_hip_gemm_ex.argtypes = [ctypes.POINTER(TvGemmArgs), ctypes.POINTER(TvEpilogue), ctypes.c_void_p]
         L.tv_hip_gemm_ex.restype = ctypes.c_int
+        L.tv_hip_gemm_noalloc.argtypes = [ctypes.POINTER(TvGemmArgs), ctypes.c_void_p]
+        L.tv_hip_gemm_noalloc.restype = ctypes.c_int
         L.tv_hip_gemv.argtypes = [ctypes.POINTER(TvGemmArgs), ctypes.c_void_p]
         L.tv_hip_gemv.restype = ctypes.c_int
         L.tv_hip_repack.argtypes = [ctypes.POINTER(TvRepackArgs), ctypes.c_void_p]

@@ -82,13 +82,14 @@ int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
     return TV_OK;
 }
 
-// Routing shared by tv_hip_gemm and tv_hip_gemm_ex.
-int run_gemm(const tv_gemm_args* args, const tvk::GemmDesc& d, hipStream_t s) {
+// Routing shared by tv_hip_gemm, tv_hip_gemm_ex and tv_hip_gemm_noalloc (fixed: the GEMV's
+// split-K buffers, nullptr for the per-stream workspace).
+int run_gemm(const tv_gemm_args* args, const tvk::GemmDesc& d, hipStream_t s, const tvk::GemvScratch* fixed = nullptr) {
     if (d.batch == 0 || d.M == 0 || d.N == 0) return TV_OK;
     if (mfma_pair(args) && d.K == 0) return tvk::launch_gemm_k0(d, s);
     if (mfma_pair(args)) {
         if (d.M <= 8) {
-            const int rc = tvk::launch_gemv(d, s);
+            const int rc = tvk::launch_gemv(d, s, fixed);
             if (rc != TV_E_UNSUPPORTED) return rc;
         }
         return tvk::launch_gemm_mfma(d, s);
@@ -114,6 +115,19 @@ int tv_hip_gemm(const tv_gemm_args* args, void* hip_stream) {
     int rc = validate(args, &d);
     if (rc) return rc;
     return run_gemm(args, d, static_cast<hipStream_t>(hip_stream));
+}
+
+int tv_hip_gemm_noalloc(const tv_gemm_args* args, void* hip_stream) {
+    int code;
+    if (take_fault(&code)) return code;
+    tvk::GemmDesc d;
+    int rc = validate(args, &d);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(hip_stream);
+    tvk::GemvScratch sc;
+    rc = tvk::gemv_static_scratch(s, &sc);
+    if (rc) return rc;
+    return run_gemm(args, d, s, &sc);
 }
 
 int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_stream) {
@@ -216,6 +230,9 @@ const char* tv_hip_strerror(int code) {
         case TV_E_UNSUPPORTED: return "tensorvia-hip: request not served by this entry point";
         case TV_E_INJECTED: return "tensorvia-hip: injected fault";
         case TV_E_NOMEM: return "tensorvia-hip: workspace allocation failed";
+        case TV_E_SCRATCH:
+            return "tensorvia-hip: the call needs more split-K scratch than tv_hip_gemm_noalloc's static buffer "
+                   "holds (4 MiB of partial slots, 16384 counters); use tv_hip_gemm";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

@@ -568,6 +568,24 @@ static int get_workspace(hipStream_t stream, size_t need, void** out, int kind) 
     return 0;
 }
 
+// Split-K buffers of one launch: the per-stream workspace (allocated and grown on demand), or the
+// caller's fixed buffers (the static scratch of tv_hip_gemm_noalloc), which must hold them.
+static int split_buffers(hipStream_t stream, const GemvScratch* fixed, int64_t nwg, size_t part_bytes, GemvArgs& g) {
+    if (fixed) {
+        if ((size_t)nwg > fixed->cnt_ints || part_bytes > fixed->part_bytes) return TV_E_SCRATCH;
+        g.cnt = fixed->cnt;
+        g.part = fixed->part;
+        return 0;
+    }
+    void* cnt = nullptr;
+    int rc = get_workspace(stream, (size_t)nwg * sizeof(int), &cnt, 1);
+    if (rc) return rc;
+    rc = get_workspace(stream, part_bytes, &g.part, 2);
+    if (rc) return rc;
+    g.cnt = static_cast<int*>(cnt);
+    return 0;
+}
+
 // Whether the vectorised GEMV serves this call.
 static bool gemv_layout_ok(const GemmDesc& d) {
     if (d.dtype_a != d.dtype_b) return false;
@@ -613,7 +631,7 @@ static GemvPlan gemv_plan(const GemmDesc& d) {
 }
 
 template <typename T, int MR, int NL, int THREADS>
-static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices) {
+static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices, const GemvScratch* fixed) {
     using Sh = GemvShape<T, MR, NL, THREADS>;
     using Acc = typename GemvTraits<T>::Acc;
     const int vec = Sh::VEC;
@@ -640,12 +658,8 @@ static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices) {
     g.cnt = nullptr;
     g.part = nullptr;
     if (S > 1) {
-        void* cnt = nullptr;
-        int rc = get_workspace(stream, (size_t)nwg * sizeof(int), &cnt, 1);
+        const int rc = split_buffers(stream, fixed, nwg, (size_t)nwg * S * MR * Sh::NB * sizeof(Acc), g);
         if (rc) return rc;
-        rc = get_workspace(stream, (size_t)nwg * S * MR * Sh::NB * sizeof(Acc), &g.part, 2);
-        if (rc) return rc;
-        g.cnt = static_cast<int*>(cnt);
     }
     hipLaunchKernelGGL((gemv_kernel<T, MR, NL, THREADS>), dim3((unsigned)nwg, S), dim3(THREADS),
                        (size_t)MR * kslice * Sh::ES, stream, g);
@@ -655,7 +669,7 @@ static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices) {
 // The matrix-core GEMV (bf16 / fp16 with 64-column strips, int8 with 128-column strips): same
 // K-slice rule as gemv_run.
 template <typename T, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
-static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices) {
+static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices, const GemvScratch* fixed) {
     using Acc = typename GemvTraits<T>::Acc;
     constexpr int ES = sizeof(T), VEC = 16 / ES, NB = 8 * VEC, CH = 64 / ES;
     // A workgroup's LDS (at most 160 KB) holds the kernel's static arrays and x's rows of a slice:
@@ -687,12 +701,8 @@ static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices) {
     g.cnt = nullptr;
     g.part = nullptr;
     if (S > 1) {
-        void* cnt = nullptr;
-        int rc = get_workspace(stream, (size_t)nwg * sizeof(int), &cnt, 1);
+        const int rc = split_buffers(stream, fixed, nwg, (size_t)nwg * S * 8 * NB * sizeof(Acc), g);
         if (rc) return rc;
-        rc = get_workspace(stream, (size_t)nwg * S * 8 * NB * sizeof(Acc), &g.part, 2);
-        if (rc) return rc;
-        g.cnt = static_cast<int*>(cnt);
     }
     const int kpad = (kslice + CH - 1) / CH * CH; // at most KCAP, a multiple of CH
     hipLaunchKernelGGL((gemv_mfma_kernel<T, WAVES, DEPTH>), dim3((unsigned)nwg, S), dim3(WAVES * 64), (size_t)8 * kpad * ES, stream, g);
@@ -701,40 +711,43 @@ static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices) {
 
 
 template <typename T, int MR>
-static int gemv_dispatch_nl(const GemmDesc& d, hipStream_t stream, const GemvPlan& p) {
+static int gemv_dispatch_nl(const GemmDesc& d, hipStream_t stream, const GemvPlan& p, const GemvScratch* fixed) {
     if (p.threads == 256) {
         switch (p.nl) {
-            case 2: return gemv_run<T, MR, 2, 256>(d, stream, p.nslices);
-            case 4: return gemv_run<T, MR, 4, 256>(d, stream, p.nslices);
-            case 8: return gemv_run<T, MR, 8, 256>(d, stream, p.nslices);
+            case 2: return gemv_run<T, MR, 2, 256>(d, stream, p.nslices, fixed);
+            case 4: return gemv_run<T, MR, 4, 256>(d, stream, p.nslices, fixed);
+            case 8: return gemv_run<T, MR, 8, 256>(d, stream, p.nslices, fixed);
         }
     } else if (p.threads == 512) {
         switch (p.nl) {
-            case 8: return gemv_run<T, MR, 8, 512>(d, stream, p.nslices);
+            case 8: return gemv_run<T, MR, 8, 512>(d, stream, p.nslices, fixed);
         }
     }
     return TV_E_UNSUPPORTED;
 }
 
 template <typename T>
-static int gemv_dispatch_mr(const GemmDesc& d, hipStream_t stream, const GemvPlan& p) {
-    if (d.M <= 1) return gemv_dispatch_nl<T, 1>(d, stream, p);
-    if (d.M <= 2) return gemv_dispatch_nl<T, 2>(d, stream, p);
-    if (d.M <= 4) return gemv_dispatch_nl<T, 4>(d, stream, p);
-    return gemv_dispatch_nl<T, 8>(d, stream, p);
+static int gemv_dispatch_mr(const GemmDesc& d, hipStream_t stream, const GemvPlan& p, const GemvScratch* fixed) {
+    if (d.M <= 1) return gemv_dispatch_nl<T, 1>(d, stream, p, fixed);
+    if (d.M <= 2) return gemv_dispatch_nl<T, 2>(d, stream, p, fixed);
+    if (d.M <= 4) return gemv_dispatch_nl<T, 4>(d, stream, p, fixed);
+    return gemv_dispatch_nl<T, 8>(d, stream, p, fixed);
+}
+
+static int launch_gemv_plan_with(const GemmDesc& d, hipStream_t stream, const GemvPlan& p, const GemvScratch* fixed) {
+    switch (d.dtype_a) {
+        case TV_FLOAT32: return gemv_dispatch_mr<float>(d, stream, p, fixed);
+        case TV_BFLOAT16: return gemv_dispatch_mr<__bf16>(d, stream, p, fixed);
+        case TV_FLOAT16: return gemv_dispatch_mr<_Float16>(d, stream, p, fixed);
+        case TV_INT8: return gemv_dispatch_mr<int8_t>(d, stream, p, fixed);
+        default: return TV_E_UNSUPPORTED;
+    }
 }
 
 int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices) {
     if (!gemv_layout_ok(d)) return TV_E_UNSUPPORTED;
     if (d.N == 0 || d.batch == 0) return 0;
-    const GemvPlan p{nl, threads, nslices};
-    switch (d.dtype_a) {
-        case TV_FLOAT32: return gemv_dispatch_mr<float>(d, stream, p);
-        case TV_BFLOAT16: return gemv_dispatch_mr<__bf16>(d, stream, p);
-        case TV_FLOAT16: return gemv_dispatch_mr<_Float16>(d, stream, p);
-        case TV_INT8: return gemv_dispatch_mr<int8_t>(d, stream, p);
-        default: return TV_E_UNSUPPORTED;
-    }
+    return launch_gemv_plan_with(d, stream, GemvPlan{nl, threads, nslices}, nullptr);
 }
 
 // The matrix-core kernel serves 16-bit W at every M and int8 W at M >= 3, with whole 128-byte
@@ -743,7 +756,7 @@ int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads,
 // M = 8 (dot 20.5) but 12.1 us at M = 1 (dot 11.5).  Its slices: about 128 KB of W per workgroup
 // (688 workgroups in all at 16 bits, 344 in int8: 4 slices of c5's K, best among 1-16), at least
 // what x's LDS slice needs, and no more than leaves each wave two chunks per slice.
-static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream) {
+static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed) {
     const int es = (int)dtype_size(d.dtype_a);
     const int nb = 128 / es, ch = 64 / es;
     const int64_t strips = (int64_t)(d.N + nb - 1) / nb * d.batch;
@@ -754,19 +767,58 @@ static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream) {
     if (s > kGemvMaxSlices) s = kGemvMaxSlices;
     // gemv_mfma_run raises s to what x's LDS slice needs
     switch (d.dtype_a) {
-        case TV_BFLOAT16: return gemv_mfma_run<__bf16>(d, stream, s);
-        case TV_FLOAT16: return gemv_mfma_run<_Float16>(d, stream, s);
-        default: return gemv_mfma_run<int8_t>(d, stream, s);
+        case TV_BFLOAT16: return gemv_mfma_run<__bf16>(d, stream, s, fixed);
+        case TV_FLOAT16: return gemv_mfma_run<_Float16>(d, stream, s, fixed);
+        default: return gemv_mfma_run<int8_t>(d, stream, s, fixed);
     }
 }
 
-int launch_gemv(const GemmDesc& d, hipStream_t stream) {
+int launch_gemv(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed) {
     if (!gemv_layout_ok(d)) return TV_E_UNSUPPORTED;
     if (d.N == 0 || d.batch == 0) return 0;
     if ((d.dtype_a == TV_BFLOAT16 || d.dtype_a == TV_FLOAT16 || (d.dtype_a == TV_INT8 && d.M >= 3)) && gemv_nl(d) == 8)
-        return launch_gemv_mfma(d, stream);
-    const GemvPlan p = gemv_plan(d);
-    return launch_gemv_plan(d, stream, p.nl, p.threads, p.nslices);
+        return launch_gemv_mfma(d, stream, fixed);
+    return launch_gemv_plan_with(d, stream, gemv_plan(d), fixed);
+}
+
+// ---- Static split-K scratch of tv_hip_gemm_noalloc ---------------------------------------------
+// One array per GPU, held until the process ends: the arrival counters (kScratchCounters ints,
+// zero between launches) followed by the partial slots (kScratchSlotBytes).  Host code never
+// passes `scratch` itself to a kernel (in host code the name is a host-side stand-in); it passes
+// the device address hipGetSymbolAddress returns for the current device, kept per device.
+constexpr size_t kScratchCounters = 16384;
+constexpr size_t kScratchCounterBytes = kScratchCounters * sizeof(int); // 64 KiB, a multiple of 256
+constexpr size_t kScratchSlotBytes = (size_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchCounterBytes + kScratchSlotBytes];
+
+constexpr int kScratchMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static unsigned char* g_scratch_ptr[kScratchMaxDevices]; // device address of `scratch` per device
+
+int gemv_static_scratch(hipStream_t stream, GemvScratch* out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kScratchMaxDevices) return TV_E_UNSUPPORTED;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!ptr) return TV_E_NULL;
+        // The counters must start at zero; every launch leaves them at zero again.  A fill kernel
+        // (not a memset node), so a caller capturing its first call records a harmless clear.
+        hipLaunchKernelGGL(gemv_zero_kernel, dim3(16), dim3(256), 0, stream, static_cast<int*>(ptr),
+                           (int64_t)kScratchCounters);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = static_cast<unsigned char*>(ptr);
+    }
+    out->cnt = reinterpret_cast<int*>(g_scratch_ptr[dev]);
+    out->cnt_ints = kScratchCounters;
+    out->part = g_scratch_ptr[dev] + kScratchCounterBytes;
+    out->part_bytes = kScratchSlotBytes;
+    return 0;
 }
 
 } // namespace tvk

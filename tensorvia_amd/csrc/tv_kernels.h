@@ -106,7 +106,21 @@ int launch_repack(const tv_repack_args* a, hipStream_t stream);
 int launch_typecast(const void* src, int src_dt, void* dst, int dst_dt, int64_t n, hipStream_t stream);
 int launch_fill(void* dst, int dt, int64_t n, float value, hipStream_t stream);
 int launch_random(void* dst, int dt, int64_t n, float min, float max, uint64_t seed, hipStream_t stream);
-int launch_gemv(const GemmDesc& d, hipStream_t stream); // TV_E_UNSUPPORTED if it does not serve d
+// Split-K buffers supplied by the caller instead of the per-stream workspace: cnt_ints arrival
+// counters (zero between launches) and part_bytes of partial slots.
+struct GemvScratch {
+    int* cnt;
+    size_t cnt_ints;
+    void* part;
+    size_t part_bytes;
+};
+// TV_E_UNSUPPORTED if it does not serve d.  fixed = nullptr: the split-K partials live in a
+// per-(device, stream) workspace that grows by hipMalloc; otherwise in *fixed (TV_E_SCRATCH when
+// they do not fit).
+int launch_gemv(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed = nullptr);
+// The static split-K scratch of the current device (set up on its first use: its address is looked
+// up and its counters cleared on `stream`).
+int gemv_static_scratch(hipStream_t stream, GemvScratch* out);
 // GEMV with an explicit strip width (nl lanes), workgroup size and K split (tuning sweeps).
 int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices);
 
