@@ -2,9 +2,17 @@
 """Benchmark of the MI355X HIP backend for Tensorvia's ops::Mul (matmul) path.
 
 One "step" is one ops::Mul call (one kernel launch) on device-resident, seeded synthetic inputs.
-The JSON line's ``value`` is configuration c2 (int8 A[4096,4096] @ B[4096,4096] -> int8 wrap), the
-configuration BASELINE.json's metric is quoted on at N=1; the other four configurations are measured
-in the same run and reported under ``configs``.
+The JSON line's ``value`` is configuration c2 (int8 A[4096,4096] @ B[4096,4096] -> int8 wrap):
+BASELINE.json's configs[1], the config the bench contract quotes at N=1 (configs[0], c1, is the
+reference's README shape, which its own CPU backend runs).  The other configurations are measured
+in the same run and reported under ``configs``, each with its own CPU baseline.
+
+Timing: W untimed launches, then K back-to-back launches in 5 runs, with HIP events on the launch
+stream at the run boundaries: the mean over all K is the per-launch time the line reports and the
+roofline uses; the median of the 5 runs' per-launch means is reported beside it.  The CPU baseline
+is the oracle's restatement of MulImpl<CPU> (src/backend/cpu/mul.cpp:97-145) on the box's host
+cores, timed with a steady clock per call as the reference's tests/mul.cpp:17-29 does, on a bounded
+sample of each workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c2,...] [--no-cpu]
                        [--only c2]   (only that config's kernel, e.g. under rocprofv3)
@@ -30,6 +38,10 @@ PEAK = {"fp32": 157.3, "bf16": 2516.6, "fp16": 2516.6, "int8": 5033.2}  # TFLOP/
 PEAK_HBM_GBS = 8000.0
 
 METRIC = "ops::matmul TFLOP/s (% MFMA peak) per dtype; GEMV HBM GB/s (% peak)"
+
+# Kernel trace of `bench.py --steps 20 --warmup 5` under rocprofv3 --kernel-trace --stats on this
+# build (profiles/bench_kernel_trace.md): per-kernel average and median durations.
+TRACE_FILE = ROOT / "profiles" / "bench_kernel_trace.json"
 
 
 def log(msg: str) -> None:
@@ -73,10 +85,23 @@ DESC = {
     "c5m8": "bf16 GEMV x[8,4096] @ W[4096,11008] -> bf16, fp32 accumulate (6 W replicas rotated)",
 }
 DTYPE = {"c1": "fp32", "c2": "int8", "c3": "bf16", "c3_fused": "bf16", "c4": "fp16", "c5m1": "bf16", "c5m8": "bf16"}
+# The kernel each configuration's launch runs.
+KERNEL = {
+    "c1": "gemm_mfma_kernel<GemmCfg<float, 128, 128, 2, 2, 0, 1>, false>",
+    "c2": "gemm_dma_kernel<GemmCfg<signed char, 256, 256, 2, 4, 0, 1>, false>",
+    "c3": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, false>",
+    "c3_fused": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, true>",
+    "c4": "gemm_smallk_kernel<GemmCfg<_Float16, 256, 256, 2, 4, 0, 0>>",
+    "c5m1": "gemv_mfma_kernel<__bf16, 4, 2>",
+    "c5m8": "gemv_mfma_kernel<__bf16, 4, 2>",
+}
+# Bound each configuration is judged against (c4's arithmetic intensity, 113.8 FLOP/B, is below
+# the fp16 ridge of about 315: HBM-bound).
+BOUND = {"c1": "mfma", "c2": "mfma", "c3": "mfma", "c3_fused": "mfma", "c4": "hbm", "c5m1": "hbm", "c5m8": "hbm"}
 
 
 def work(name: str, inp) -> tuple[float, float]:
-    """(algorithmic flops/ops, algorithmic HBM bytes) per call."""
+    """(algorithmic flops/ops, algorithmic HBM bytes) per call: each operand read once, C written once."""
     a, b = inp["a"], inp["b"]
     es = a.itemsize
     if name == "c4":
@@ -88,8 +113,42 @@ def work(name: str, inp) -> tuple[float, float]:
     else:
         B, (M, K) = 1, a.shape
     N = b.shape[-1]
-    out_es = es
-    return 2.0 * B * M * N * K, (a.size + b.size) * es + B * M * N * out_es
+    return 2.0 * B * M * N * K, (a.size + b.size) * es + B * M * N * es
+
+
+def timed_launches(launch, steps: int, warmup: int, stream, groups: int = 5):
+    """W untimed launches, then K back-to-back launches in `groups` runs of consecutive launches,
+    with a HIP event on the launch stream at each run boundary.  Returns the mean per-launch time
+    over the whole timed region, the median over the runs of their per-launch means, and the host
+    wall time per step."""
+    import torch
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    groups = max(1, min(groups, steps))
+    bounds = [round(g * steps / groups) for g in range(groups + 1)]
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
+    t0 = time.perf_counter()
+    evs[0].record(stream)
+    for g in range(groups):
+        for i in range(bounds[g], bounds[g + 1]):
+            launch(i)
+        evs[g + 1].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    mean_ms = evs[0].elapsed_time(evs[-1]) / steps
+    median_ms = float(np.median([evs[g].elapsed_time(evs[g + 1]) / (bounds[g + 1] - bounds[g]) for g in range(groups)]))
+    return mean_ms, median_ms, wall_ms
+
+
+def rates(res: dict, name: str) -> dict:
+    ms = res["kernel_ms_mean"]
+    res["tflops"] = res["flops"] / (ms * 1e-3) / 1e12
+    res["tflops_frac_peak"] = res["tflops"] / PEAK[DTYPE[name]]
+    res["hbm_gbs"] = res["algorithmic_bytes"] / (ms * 1e-3) / 1e9
+    res["hbm_frac_peak"] = res["hbm_gbs"] / PEAK_HBM_GBS
+    res["roofline_frac"] = res["tflops_frac_peak"] if BOUND[name] == "mfma" else res["hbm_frac_peak"]
+    return res
 
 
 def run_gpu(name: str, steps: int, warmup: int):
@@ -112,8 +171,8 @@ def run_gpu(name: str, steps: int, warmup: int):
         reps = [b] + [b.clone() for _ in range(5)]
     out = tv.gemm(a, b)  # allocates the output (and any workspace) outside the timed region
     torch.cuda.synchronize()
-    # Descriptors are packed once: the timed loop is one C-ABI call per step, so the host enqueues
-    # launches faster than the GPU retires them and the events bracket back-to-back kernels.
+    # Descriptors are packed once: a step is one C-ABI call, so the host enqueues launches faster
+    # than the GPU retires them and the events bracket back-to-back kernels.
     L = tv.lib()
     descs = [tv.make_args(a, r, out) for r in reps]
     stream = torch.cuda.current_stream()
@@ -124,7 +183,7 @@ def run_gpu(name: str, steps: int, warmup: int):
         ep = tv.TvEpilogue()
         ep.act, ep.bias, ep.sbias_b, ep.sbias_m, ep.sbias_n = tv.ACT_SILU, bias.data_ptr(), 0, 0, 1
 
-    def step(i):
+    def launch(i):
         if ep is None:
             rc = L.tv_hip_gemm(ctypes.byref(descs[i % len(descs)]), sh)
         else:
@@ -132,32 +191,12 @@ def run_gpu(name: str, steps: int, warmup: int):
         if rc:
             tv.check(rc)
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for i in range(steps):
-        step(i)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    per_launch_ms = ev0.elapsed_time(ev1) / steps
+    mean_ms, median_ms, wall_ms = timed_launches(launch, steps, warmup, stream)
     flops, bytes_ = work(name, inp)
-    res = {
-        "workload": DESC[name],
-        "dtype": DTYPE[name],
-        "kernel_ms_mean": float(per_launch_ms),
-        "ms_per_step": wall_ms,
-        "flops": flops,
-        "algorithmic_bytes": bytes_,
-    }
-    res["tflops"] = flops / (res["kernel_ms_mean"] * 1e-3) / 1e12
-    res["tflops_frac_peak"] = res["tflops"] / PEAK[DTYPE[name]]
-    res["hbm_gbs"] = bytes_ / (res["kernel_ms_mean"] * 1e-3) / 1e9
-    res["hbm_frac_peak"] = res["hbm_gbs"] / PEAK_HBM_GBS
+    res = {"workload": DESC[name], "dtype": DTYPE[name], "bound": BOUND[name], "kernel": KERNEL[name],
+           "kernel_ms_mean": float(mean_ms), "kernel_ms_median_of_runs": median_ms, "ms_per_step": wall_ms,
+           "flops": flops, "algorithmic_bytes": bytes_}
+    rates(res, name)
     del a, b, reps, out
     torch.cuda.empty_cache()
     return res, inp
@@ -177,11 +216,11 @@ def run_vendor(name: str, inp, steps: int, warmup: int) -> dict:
     b = to_torch(inp["b"], dt)
     note = "torch.matmul"
     if name == "c2":
-        fn = lambda i: torch._int_mm(a, b)
+        fn = lambda i: torch._int_mm(a, b)  # noqa: E731
         note = "torch._int_mm (int32 output)"
     elif name == "c4":
         bt = b.permute(0, 2, 1).contiguous()
-        fn = lambda i: torch.bmm(a, bt)
+        fn = lambda i: torch.bmm(a, bt)  # noqa: E731
         note = "torch.bmm with K^T materialised"
     elif "bias" in inp:
         bias = to_torch(inp["bias"], dt)
@@ -189,23 +228,14 @@ def run_vendor(name: str, inp, steps: int, warmup: int) -> dict:
         note = "torch.nn.functional.silu(torch.matmul(a, b) + bias) (three kernels)"
     else:
         reps = [b] + ([b.clone() for _ in range(5)] if name.startswith("c5") else [])
-        fn = lambda i: torch.matmul(a, reps[i % len(reps)])
+        fn = lambda i: torch.matmul(a, reps[i % len(reps)])  # noqa: E731
         if name.startswith("c5"):
             note = "torch.matmul, 6 W replicas rotated"
-    for i in range(warmup):
-        fn(i)
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for i in range(steps):
-        fn(i)
-    ev1.record()
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / steps
+    mean_ms, median_ms, _ = timed_launches(fn, steps, warmup, torch.cuda.current_stream())
     flops, bytes_ = work(name, inp)
-    res = {"call": note, "ms_mean": ms, "tflops": flops / (ms * 1e-3) / 1e12,
-           "tflops_frac_peak": flops / (ms * 1e-3) / 1e12 / PEAK[DTYPE[name]], "hbm_gbs": bytes_ / (ms * 1e-3) / 1e9}
+    res = {"call": note, "ms_mean": mean_ms, "ms_median_of_runs": median_ms, "tflops": flops / (mean_ms * 1e-3) / 1e12,
+           "tflops_frac_peak": flops / (mean_ms * 1e-3) / 1e12 / PEAK[DTYPE[name]],
+           "hbm_gbs": bytes_ / (mean_ms * 1e-3) / 1e9}
     torch.cuda.empty_cache()
     return res
 
@@ -226,7 +256,8 @@ def run_ew(name: str, steps: int, warmup: int) -> dict:
     import tensorvia_amd as tv
     L = tv.lib()
     n = 16 * 2048 * 4096
-    sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
     if name == "cast_c3a":
         # Two sources (2 x 268 MB) taken in turn, so that no call finds its source in the 256 MB
         # MALL (Infinity Cache) from the call before.
@@ -234,16 +265,14 @@ def run_ew(name: str, steps: int, warmup: int) -> dict:
         for s_ in srcs:
             tv.check(L.tv_hip_random(ctypes.c_void_p(s_.data_ptr()), tv.BFLOAT16, n, -1.0, 1.0, 5, sh))
         dst = torch.empty(n, dtype=torch.float32, device="cuda")
-        turn = [0]
 
-        def call():
-            turn[0] ^= 1
-            return L.tv_hip_typecast(ctypes.c_void_p(srcs[turn[0]].data_ptr()), tv.BFLOAT16,
+        def call(i):
+            return L.tv_hip_typecast(ctypes.c_void_p(srcs[i & 1].data_ptr()), tv.BFLOAT16,
                                      ctypes.c_void_p(dst.data_ptr()), tv.FLOAT32, n, sh)
         nbytes = n * 2 + n * 4
     elif name == "random_c3a":
         dst = torch.empty(n, dtype=torch.int16, device="cuda")
-        call = lambda: L.tv_hip_random(ctypes.c_void_p(dst.data_ptr()), tv.BFLOAT16, n, -1.0, 1.0, 5, sh)  # noqa: E731
+        call = lambda i: L.tv_hip_random(ctypes.c_void_p(dst.data_ptr()), tv.BFLOAT16, n, -1.0, 1.0, 5, sh)  # noqa: E731
         nbytes = n * 2
     elif name == "transpose_c4k":
         m = 32 * 2048 * 128
@@ -255,26 +284,24 @@ def run_ew(name: str, steps: int, warmup: int) -> dict:
         for d, (ext, st) in enumerate(zip((32, 128, 2048), (2048 * 128, 1, 128))):
             a.shape[d], a.strides[d] = ext, st
         a.src, a.dst = src.data_ptr(), dst.data_ptr()
-        call = lambda: L.tv_hip_repack(ctypes.byref(a), sh)  # noqa: E731
+        call = lambda i: L.tv_hip_repack(ctypes.byref(a), sh)  # noqa: E731
         nbytes = m * 2 * 2
     else:
         dst = torch.empty(n, dtype=torch.float32, device="cuda")
-        call = lambda: L.tv_hip_fill(ctypes.c_void_p(dst.data_ptr()), tv.FLOAT32, n, 1.0, sh)  # noqa: E731
+        call = lambda i: L.tv_hip_fill(ctypes.c_void_p(dst.data_ptr()), tv.FLOAT32, n, 1.0, sh)  # noqa: E731
         nbytes = n * 4
-    for _ in range(warmup):
-        tv.check(call())
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(steps):
-        call()
-    ev1.record()
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / steps
-    res = {"workload": EW[name], "kernel_ms_mean": ms, "algorithmic_bytes": nbytes,
-           "hbm_gbs": nbytes / (ms * 1e-3) / 1e9}
+    tv.check(call(0))
+
+    def launch(i):
+        rc = call(i)
+        if rc:
+            tv.check(rc)
+
+    mean_ms, median_ms, _ = timed_launches(launch, steps, warmup, stream)
+    res = {"workload": EW[name], "bound": "hbm", "kernel_ms_mean": mean_ms, "kernel_ms_median_of_runs": median_ms,
+           "algorithmic_bytes": nbytes, "hbm_gbs": nbytes / (mean_ms * 1e-3) / 1e9}
     res["hbm_frac_peak"] = res["hbm_gbs"] / PEAK_HBM_GBS
+    res["roofline_frac"] = res["hbm_frac_peak"]
     del dst
     torch.cuda.empty_cache()
     return res
@@ -287,50 +314,81 @@ def run_copy(steps: int, warmup: int) -> dict:
     n = 512 << 20
     src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
-    for _ in range(warmup):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(steps):
-        dst.copy_(src)
-    ev1.record()
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / steps
+    mean_ms, median_ms, _ = timed_launches(lambda i: dst.copy_(src), steps, warmup, torch.cuda.current_stream())
     return {"workload": "device copy of 512 MiB (uint8)", "bytes_read": n, "bytes_written": n,
-            "kernel_ms_mean": ms, "hbm_gbs": 2 * n / (ms * 1e-3) / 1e9}
+            "kernel_ms_mean": mean_ms, "hbm_gbs": 2 * n / (mean_ms * 1e-3) / 1e9}
 
 
-def run_cpu(name: str, inp, iters: int):
+# CPU baseline per configuration: calls timed and the sample of the workload they run.  c3's full
+# call is about a minute of CPU time on 16 threads, so it runs as the flattened 2-d call on 4 of
+# the 16 batches (8,192 rows; the reference rejects the broadcast form, and its tiled kernel does
+# the same work per row for any row count); c4 multiplies by a pre-materialised K^T (the CPU kernel
+# ignores strides), whose transpose is timed apart.
+CPU_PLAN = {"c1": (3, None), "c2": (3, None), "c3": (1, 4), "c4": (3, None), "c5m1": (10, None), "c5m8": (10, None)}
+
+
+def cpu_effective_threads(threads: int, batch: int, M: int, N: int) -> int:
+    """OpenMP threads with work under the reference's schedule (mul.cpp:87-96): the basic kernel
+    (batch*M*N < 2^20) parallelises batch*M rows, the tiled kernel batch x 64-row x 64-column tiles."""
+    if batch * M * N < (1 << 20):
+        return min(threads, batch * M)
+    return min(threads, batch * -(-M // 64) * -(-N // 64))
+
+
+def run_cpu(name: str, inp) -> dict:
     import oracle
     a, b, dt = inp["a"], inp["b"], inp["dt"]
-    note = ""
-    t_extra = 0.0
+    iters, batches = CPU_PLAN[name]
+    note = "full workload"
+    extra = {}
+    flops_full, _ = work(name, inp)
+    flops = flops_full
     if name == "c3":
-        a = a.reshape(-1, a.shape[-1])  # the reference rejects the broadcast form: flattened 2-D call
-        note = "flattened [32768,4096]@[4096,4096]"
+        a = a[:batches].reshape(-1, a.shape[-1])
+        flops = flops_full * batches / inp["a"].shape[0]
+        note = f"flattened 2-d call on {batches} of the 16 batches: [{a.shape[0]},4096]@[4096,4096]"
     if name == "c4":
         t = time.perf_counter()
-        b = oracle.transpose_last2(b)  # ops::Transpose(K,{0,2,1}): the CPU matmul ignores strides
-        t_extra = time.perf_counter() - t
-        note = f"pre-materialised K^T (transpose {t_extra * 1e3:.1f} ms, excluded)"
-    oracle.mul(a[:8], dt, b, dt) if a.ndim == 2 else None  # page in / thread pool warm-up
+        b = oracle.transpose_last2(b)  # ops::Transpose(K,{0,2,1})
+        extra["transpose_ms"] = (time.perf_counter() - t) * 1e3
+        note = f"full workload on a pre-materialised K^T (its transpose {extra['transpose_ms']:.1f} ms, not in the time)"
+    oracle.mul(a[..., :8, :], dt, b, dt)  # page in / thread pool warm-up
     times = []
-    t_start = time.perf_counter()
-    # At least `iters` calls, continuing until about 10 s of CPU time has been measured.
-    while len(times) < iters or (time.perf_counter() - t_start < 10.0 and len(times) < 50):
+    for _ in range(iters):
         t = time.perf_counter()
         oracle.mul(a, dt, b, dt)
         times.append(time.perf_counter() - t)
-    iters = len(times)
-    flops, _ = work(name, inp)
-    s = float(np.mean(times))
-    return {"value": flops / s / 1e12, "unit": "TFLOP/s" if DTYPE[name] != "int8" else "TOP/s",
-            "seconds": s, "iters": iters, "cores": oracle.threads_used(), "kind": "port",
-            "sample": f"full {name} workload, {iters} iteration(s), oracle restatement of MulImpl<CPU> "
-                      f"(tiled/basic as the reference selects, 16-thread cap){'; ' + note if note else ''}",
-            "nproc": os.cpu_count(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+    s = float(np.median(times))
+    threads = oracle.threads_used()
+    batch = a.shape[0] if a.ndim == 3 else 1
+    eff = cpu_effective_threads(threads, batch, a.shape[-2], b.shape[-1])
+    unit = "TOP/s" if DTYPE[name] == "int8" else "TFLOP/s"
+    return {"value": flops / s / 1e12, "unit": unit, "cores": eff, "kind": "port",
+            "sample": f"{name}: {note}; {iters} call(s), median; oracle restatement of MulImpl<CPU> "
+                      f"(basic/tiled as the reference selects, fp16/bf16 widening included)",
+            "seconds_median": s, "iters": iters, "nproc": os.cpu_count(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "openmp_threads": threads,
+            "effective_threads": eff, **extra}
+
+
+def trace_check(name: str, res: dict) -> dict | None:
+    """The committed kernel trace's figures for this config's kernel, beside the live ones."""
+    if not TRACE_FILE.exists() or name not in KERNEL:
+        return None
+    tr = json.loads(TRACE_FILE.read_text())
+    k = tr.get("configs", {}).get(name)
+    if not k:
+        return None
+    trace_ms = k["avg_ns"] * 1e-6
+    out = {"trace_file": str(TRACE_FILE.relative_to(ROOT)), "trace_avg_ms": trace_ms,
+           "trace_median_ms": k.get("median_ns", k["avg_ns"]) * 1e-6,
+           "trace_vs_live": trace_ms / res["kernel_ms_mean"],
+           "trace_exceeds_ms_per_step": trace_ms > res["ms_per_step"]}
+    if BOUND[name] == "mfma":
+        out["frac_from_trace"] = res["flops"] / (trace_ms * 1e-3) / 1e12 / PEAK[DTYPE[name]]
+    else:
+        out["frac_from_trace"] = res["algorithmic_bytes"] / (trace_ms * 1e-3) / 1e9 / PEAK_HBM_GBS
+    return out
 
 
 def main() -> int:
@@ -341,8 +399,7 @@ def main() -> int:
     ap.add_argument("--configs", default="c1,c2,c3,c3_fused,c4,c5m1,c5m8,cast_c3a,random_c3a,fill_c3a,transpose_c4k")
     ap.add_argument("--only", default=None,
                     help="run only this config's GPU kernel (for profilers); 'copy' runs the traffic calibration copy")
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-all", action="store_true", help="CPU baseline for every config, not only c2")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--vendor", action="store_true", help="also time torch's library GEMM on the same inputs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -373,32 +430,41 @@ def main() -> int:
             continue
         log(f"gpu {n}: {DESC[n]}")
         results[n], inputs[n] = run_gpu(n, args.steps, args.warmup)
-        log(f"gpu {n}: {results[n]['kernel_ms_mean'] * 1e3:.1f} us  {results[n]['tflops']:.1f} T/s  "
-            f"{results[n]['hbm_gbs']:.0f} GB/s")
+        r = results[n]
+        log(f"gpu {n}: {r['kernel_ms_mean'] * 1e3:.1f} us mean, {r['kernel_ms_median_of_runs'] * 1e3:.1f} us median "
+            f"of 5 runs  {r['tflops']:.1f} T/s  {r['hbm_gbs']:.0f} GB/s  roofline {r['roofline_frac']:.3f}")
+        tc = trace_check(n, r)
+        if tc:
+            r["profile"] = tc
         if args.vendor:
             v = run_vendor(n, inputs[n], args.steps, args.warmup)
-            results[n]["torch_library"] = v
+            r["torch_library"] = v
             log(f"torch {n}: {v['ms_mean'] * 1e3:.1f} us  {v['tflops']:.1f} T/s  {v['hbm_gbs']:.0f} GB/s  ({v['call']})")
     if args.only:
         print(json.dumps({"only": args.only, **results[args.only]}))
         return 0
 
-    head = results["c2"]
-    cpu = None
     if not args.no_cpu:
-        log("cpu baseline c2 (oracle)")
-        cpu = run_cpu("c2", inputs["c2"], iters=3)
-        log(f"cpu c2: {cpu['seconds']:.2f} s, {cpu['value'] * 1e3:.1f} GOP/s on {cpu['cores']} threads")
-        if args.cpu_all:
-            for n in names:
-                if n != "c2" and n not in EW and n != "c3_fused":
-                    log(f"cpu baseline {n}")
-                    results[n]["cpu_baseline"] = run_cpu(n, inputs[n], iters=1)
+        for n in names:
+            if n in CPU_PLAN and n in inputs:
+                log(f"cpu baseline {n} (oracle)")
+                results[n]["cpu_baseline"] = c = run_cpu(n, inputs[n])
+                log(f"cpu {n}: {c['seconds_median']:.3f} s per call, {c['value'] * 1e3:.2f} G/s, "
+                    f"{c['openmp_threads']} OpenMP threads, {c['effective_threads']} with work")
 
+    head = results["c2"]
     traffic = None
     tf = ROOT / "profiles" / "gemm_int8_c2_traffic.json"
     if tf.exists():
         traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+    roof = {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK["int8"], "unit": "TOP/s",
+            "frac": head["tflops_frac_peak"], "traffic": traffic,
+            "kernel": "gemm_dma_kernel<int8, 256x256 tile, 2-stage global->LDS DMA, A k-contiguous, B n-contiguous>",
+            "per_launch_ms": head["kernel_ms_mean"], "per_launch_ms_median_of_runs": head["kernel_ms_median_of_runs"],
+            "achieved_basis": "algorithmic ops / mean launch duration over the timed region (HIP events on the launch stream)"}
+    if "profile" in head:
+        roof["profile"] = head["profile"]
+    cpu = head.get("cpu_baseline")
     line = {
         "metric": METRIC,
         "value": head["flops"] / (head["ms_per_step"] * 1e-3) / 1e12,
@@ -412,12 +478,11 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic: seeded counter-based generator (SplitMix64), uniform ints in [-10,10]",
-        "config": {"workload": "c2: " + DESC["c2"], "M": 4096, "N": 4096, "K": 4096, "accumulate": "int32"},
-        "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK["int8"], "unit": "TOP/s",
-                     "frac": head["tflops_frac_peak"], "traffic": traffic,
-                     "kernel": "gemm_dma_kernel<int8, 256x256 tile, 2-stage global->LDS DMA, A k-contiguous, B n-contiguous>",
-                     "per_launch_ms": head["kernel_ms_mean"]},
-        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "config": {"workload": "c2: " + DESC["c2"], "M": 4096, "N": 4096, "K": 4096, "accumulate": "int32",
+                   "why": "BASELINE.json configs[1], the single-GPU config the metric is quoted on"},
+        "roofline": roof,
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in (
+            "value", "unit", "cores", "kind", "sample", "nproc", "omp_num_threads", "openmp_threads", "effective_threads")},
         "configs": results,
     }
     print(json.dumps(line))
