@@ -5,12 +5,43 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <condition_variable>
 #include <memory>
 #include <mutex>
+#include <thread>
+#include <vector>
 
 #include "context.h"
 #include "ops.h"
 #include "tensor.h"
+
+// memcpy split over a small pool of host threads in page-aligned parts (the host side of the
+// pinned staging copies; one thread moves pageable memory at about half the DMA engines' rate).
+class ParallelMemcpy {
+public:
+    static constexpr size_t kMinSplit = size_t(1) << 20; // smaller copies stay on the calling thread
+    explicit ParallelMemcpy(int threads = 0);            // 0: min(8, hardware threads)
+    ~ParallelMemcpy();
+    ParallelMemcpy(const ParallelMemcpy&) = delete;
+    ParallelMemcpy& operator=(const ParallelMemcpy&) = delete;
+    // Returns when all n bytes are copied.  One copy at a time per object.
+    void copy(void* dst, const void* src, size_t n);
+    int threads() const { return m_threads; }
+
+private:
+    void work(int i);
+    void copy_part(int i) const;
+    int m_threads = 1;
+    std::vector<std::thread> m_workers;
+    std::mutex m_mu;
+    std::condition_variable m_go, m_fin;
+    char* m_dst = nullptr;
+    const char* m_src = nullptr;
+    size_t m_len = 0, m_part = 0;
+    unsigned m_gen = 0;
+    int m_left = 0;
+    bool m_stop = false;
+};
 
 // One HIP device (the one with the most memory, as CUDAContext picks, cuda_context.h:14-36) and
 // one stream.  Ops enqueue on the stream and synchronise it before returning.

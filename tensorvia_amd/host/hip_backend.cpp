@@ -51,6 +51,66 @@ HIPContext::HIPContext() {
     hip_check(hipStreamCreate(&m_stream), "hipStreamCreate");
 }
 
+// ---- ParallelMemcpy ------------------------------------------------------------------------------
+
+ParallelMemcpy::ParallelMemcpy(int threads) {
+    if (threads <= 0) {
+        const unsigned hw = std::thread::hardware_concurrency();
+        threads = static_cast<int>(std::min(8u, hw ? hw : 1u));
+    }
+    m_threads = threads;
+    for (int i = 1; i < m_threads; ++i) m_workers.emplace_back([this, i] { work(i); });
+}
+
+ParallelMemcpy::~ParallelMemcpy() {
+    {
+        std::lock_guard<std::mutex> lk(m_mu);
+        m_stop = true;
+    }
+    m_go.notify_all();
+    for (auto& t : m_workers) t.join();
+}
+
+// Part i of the current job: [i * part, (i + 1) * part) clipped to the job's length.
+void ParallelMemcpy::copy_part(int i) const {
+    const size_t b = std::min(m_len, i * m_part), e = std::min(m_len, (i + 1) * m_part);
+    if (e > b) std::memcpy(m_dst + b, m_src + b, e - b);
+}
+
+void ParallelMemcpy::work(int i) {
+    unsigned seen = 0;
+    std::unique_lock<std::mutex> lk(m_mu);
+    for (;;) {
+        m_go.wait(lk, [&] { return m_stop || m_gen != seen; });
+        if (m_stop) return;
+        seen = m_gen;
+        lk.unlock();
+        copy_part(i);
+        lk.lock();
+        if (--m_left == 0) m_fin.notify_one();
+    }
+}
+
+void ParallelMemcpy::copy(void* dst, const void* src, size_t n) {
+    if (m_threads == 1 || n < kMinSplit) {
+        if (n) std::memcpy(dst, src, n);
+        return;
+    }
+    std::unique_lock<std::mutex> lk(m_mu);
+    m_dst = static_cast<char*>(dst);
+    m_src = static_cast<const char*>(src);
+    m_len = n;
+    // ceil(n / threads) rounded up to whole pages, so the parts cover all n bytes.
+    m_part = ((n + m_threads - 1) / m_threads + 4095) & ~size_t(4095);
+    m_left = m_threads - 1;
+    ++m_gen;
+    lk.unlock();
+    m_go.notify_all();
+    copy_part(0);
+    lk.lock();
+    m_fin.wait(lk, [&] { return m_left == 0; });
+}
+
 // Two pinned chunks, the events that mark the DMA last issued from each, and the host threads that
 // split each chunk's memcpy (one thread copies a pageable buffer at about half the rate the DMA
 // engines move a pinned one).
@@ -58,72 +118,15 @@ struct HIPContext::Staging {
     static constexpr size_t kChunk = size_t(16) << 20;
     void* buf[2] = {nullptr, nullptr};
     hipEvent_t done[2] = {nullptr, nullptr};
+    ParallelMemcpy mc;
 
-    int nthreads = 1;
-    std::vector<std::thread> workers;
-    std::mutex mu;
-    std::condition_variable go, fin;
-    char* job_dst = nullptr;
-    const char* job_src = nullptr;
-    size_t job_len = 0, job_part = 0;
-    unsigned gen = 0;
-    int left = 0;
-    bool stop = false;
-
-    Staging() {
-        const unsigned hw = std::thread::hardware_concurrency();
-        nthreads = static_cast<int>(std::min(8u, hw ? hw : 1u));
-        for (int i = 1; i < nthreads; ++i) workers.emplace_back([this, i] { work(i); });
-    }
     ~Staging() {
-        {
-            std::lock_guard<std::mutex> lk(mu);
-            stop = true;
-        }
-        go.notify_all();
-        for (auto& t : workers) t.join();
         for (int i = 0; i < 2; ++i) {
             if (done[i]) (void)hipEventDestroy(done[i]);
             if (buf[i]) (void)hipHostFree(buf[i]);
         }
     }
-    // Part i of the current job: [i * job_part, (i + 1) * job_part) clipped to job_len.
-    void copy_part(int i) const {
-        const size_t b = std::min(job_len, i * job_part), e = std::min(job_len, (i + 1) * job_part);
-        if (e > b) std::memcpy(job_dst + b, job_src + b, e - b);
-    }
-    void work(int i) {
-        unsigned seen = 0;
-        std::unique_lock<std::mutex> lk(mu);
-        for (;;) {
-            go.wait(lk, [&] { return stop || gen != seen; });
-            if (stop) return;
-            seen = gen;
-            lk.unlock();
-            copy_part(i);
-            lk.lock();
-            if (--left == 0) fin.notify_one();
-        }
-    }
-    // memcpy split over the threads in page-aligned parts; returns when every part is done.
-    void copy(void* dst, const void* src, size_t n) {
-        if (nthreads == 1 || n < (size_t(1) << 20)) {
-            std::memcpy(dst, src, n);
-            return;
-        }
-        std::unique_lock<std::mutex> lk(mu);
-        job_dst = static_cast<char*>(dst);
-        job_src = static_cast<const char*>(src);
-        job_len = n;
-        job_part = (n / nthreads + 4095) & ~size_t(4095);
-        left = nthreads - 1;
-        ++gen;
-        lk.unlock();
-        go.notify_all();
-        copy_part(0);
-        lk.lock();
-        fin.wait(lk, [&] { return left == 0; });
-    }
+    void copy(void* dst, const void* src, size_t n) { mc.copy(dst, src, n); }
 };
 
 // Copies below this size go straight through hipMemcpyAsync.

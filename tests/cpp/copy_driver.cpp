@@ -66,8 +66,11 @@ void check(hipError_t e, const char* what) {
 int main(int argc, char** argv) {
     int failures = 0;
     const size_t MiB = size_t(1) << 20;
+    // 24 MiB + 5 and 17 MiB + 4 end in a staged chunk whose length over the 8 memcpy threads has a
+    // page-aligned quotient (8 MiB + 5, 1 MiB + 4): the sizes whose tail a floor-rounded part size
+    // would drop.
     for (size_t bytes : {size_t(1), size_t(1000), 4 * MiB - 1, 4 * MiB, 16 * MiB, 16 * MiB + 3, 32 * MiB + 17,
-                         40 * MiB + 12345})
+                         40 * MiB + 12345, 24 * MiB + 5, 17 * MiB + 4})
         failures += round_trip(bytes, static_cast<uint32_t>(bytes)) ? 0 : 1;
 
     if (argc == 3 && std::string(argv[1]) == "--time") {

@@ -1,8 +1,9 @@
 // Host-side checks of the C++ API that need no GPU: views and offsets, CPU gathers, ops::Mul
-// validation, Typecast, and the seeded generator (its stream is written to <outdir> for the
+// validation, Typecast, the staging copies' threaded memcpy, and the seeded generator (its stream is written to <outdir> for the
 // Python side to compare against tensorvia_amd/rng.py).
 //
 // Usage: host_api_test <outdir>.  Prints "ok <name>" per check; exits non-zero on the first failure.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -11,6 +12,7 @@
 #include <string>
 #include <vector>
 
+#include "tensorvia/hip_backend.h"
 #include "tensorvia/ops.h"
 
 using via::DataType;
@@ -159,6 +161,23 @@ int main(int argc, char** argv) {
                      "transpose shape and axes size not match");
         // Valid shapes on CPU tensors: the CPU backend is not part of this build.
         expect_throw("mul_validation_messages", [&] { ops::Mul(a2, b2); }, "to_device");
+    });
+
+    run("parallel_memcpy", [] {
+        // The staging copies' threaded memcpy: every byte copied, nothing written past the end, at
+        // sizes around the split threshold and the page-aligned part boundaries.
+        for (int threads : {1, 2, 3, 8}) {
+            ParallelMemcpy mc(threads);
+            for (size_t n : {size_t(0), size_t(1), size_t(4095), ParallelMemcpy::kMinSplit - 1, ParallelMemcpy::kMinSplit,
+                             ParallelMemcpy::kMinSplit + 7, (size_t(3) << 20) + 123, (size_t(16) << 20) + 5}) {
+                std::vector<unsigned char> src(n + 64), dst(n + 64, 0xA5);
+                for (size_t i = 0; i < src.size(); ++i) src[i] = static_cast<unsigned char>(i * 131 + 7);
+                mc.copy(dst.data(), src.data(), n);
+                bool ok = std::equal(src.begin(), src.begin() + static_cast<std::ptrdiff_t>(n), dst.begin());
+                for (size_t i = n; i < n + 64; ++i) ok = ok && dst[i] == 0xA5;
+                check(ok, "parallel_memcpy", "threads " + std::to_string(threads) + " bytes " + std::to_string(n));
+            }
+        }
     });
 
     run("typecast_widening_exact", [] {

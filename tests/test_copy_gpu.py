@@ -11,7 +11,8 @@ from tests.cpp import build as cpp
 
 pytestmark = pytest.mark.gpu
 
-SIZES = [1, 1000, 4 * 2**20 - 1, 4 * 2**20, 16 * 2**20, 16 * 2**20 + 3, 32 * 2**20 + 17, 40 * 2**20 + 12345]
+SIZES = [1, 1000, 4 * 2**20 - 1, 4 * 2**20, 16 * 2**20, 16 * 2**20 + 3, 32 * 2**20 + 17, 40 * 2**20 + 12345,
+         24 * 2**20 + 5, 17 * 2**20 + 4]
 
 
 @pytest.fixture(scope="module")

@@ -17,7 +17,7 @@ def host_run(tmp_path_factory):
 
 
 @pytest.mark.parametrize("check", ["transpose_view_strides", "slice_offset_and_gather", "permute_021_like_config4",
-                                   "copy_of_view_is_contiguous", "mul_validation_messages",
+                                   "copy_of_view_is_contiguous", "mul_validation_messages", "parallel_memcpy",
                                    "typecast_widening_exact", "random_streams_dumped"])
 def test_host_api_check(host_run, check):
     r, _ = host_run
@@ -62,3 +62,17 @@ def test_libtensorvia_exports_the_plugin_api():
                 "ops::TransposeImpl<(via::Device)4>::execute(Tensor const&, Tensor&, std::initializer_list<long>)",
                 "ops::Typecast(Tensor const&, via::DataType)"]:
         assert sym in names, sym
+
+
+@pytest.mark.parametrize("exe,env", [("host_api_test_asan", {"ASAN_OPTIONS": "detect_leaks=1:abort_on_error=0",
+                                                             "UBSAN_OPTIONS": "print_stacktrace=1"}),
+                                     ("host_api_test_tsan", {"TSAN_OPTIONS": "halt_on_error=1"})])
+def test_host_api_under_sanitizers(tmp_path, exe, env):
+    """The same host checks built with the host sources of libtensorvia.so under AddressSanitizer +
+    UndefinedBehaviorSanitizer (leak detection on) and under ThreadSanitizer: every check passes and
+    no sanitizer reports (tests/cpp/build.py --sanitize builds them; CPU only)."""
+    import os
+    r = subprocess.run([str(cpp.binary(exe)), str(tmp_path)], capture_output=True, text=True, timeout=300,
+                       env={**os.environ, **env})
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
+    assert "FAIL" not in r.stdout and "Sanitizer" not in r.stderr and "runtime error" not in r.stderr, r.stderr[-3000:]
