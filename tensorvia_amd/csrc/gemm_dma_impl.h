@@ -432,6 +432,17 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
         lds_barrier();
         char* lw = (wave < NWAVES / 2 ? S0 : S1) + (wave % (NWAVES / 2)) * EPI;
         const int mrow0 = m0 + wm * C::WM, ncol0 = n0 + wn * C::WN;
+        if (c_vec == 2 && (d.bias == nullptr || d.sbias_m == 0)) {
+            // per-column (or no) bias: applied as the accumulators are staged by the plain store
+            auto store = [&](const auto& f) {
+                if (d.dtype_c == TV_BFLOAT16) write_tile_staged<__bf16, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d, f);
+                else if (d.dtype_c == TV_FLOAT16) write_tile_staged<_Float16, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d, f);
+                else write_tile_staged<float, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d, f);
+            };
+            if (d.act == TV_ACT_SILU || d.act == TV_ACT_SIGMOID || d.act == TV_ACT_TANH) store(ColBiasAct<C::FN, true>(d, b, ncol0, lane));
+            else store(ColBiasAct<C::FN, false>(d, b, ncol0, lane));
+            return;
+        }
         if (d.dtype_c == TV_BFLOAT16) write_tile_staged_epi<__bf16, C, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d, b, c_vec != 0);
         else if (d.dtype_c == TV_FLOAT16) write_tile_staged_epi<_Float16, C, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d, b, c_vec != 0);
         else write_tile_staged_epi<float, C, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d, b, c_vec != 0);

@@ -323,9 +323,14 @@ template <int WM, int PITCH, int WAVE_BYTES> constexpr int staged_rows() {
     return r;
 }
 
-template <typename TC, class C, typename Acc, int WAVE_BYTES = kEpiWaveBytes>
+// Value transform of the staged store: identity for a plain matmul.
+struct NoTransform {
+    template <typename V> __device__ V operator()(V v, int, int) const { return v; }
+};
+
+template <typename TC, class C, typename Acc, int WAVE_BYTES = kEpiWaveBytes, class F = NoTransform>
 __device__ inline void write_tile_staged(const Acc (&acc)[C::FM][C::FN], char* lds_wave, char* Cb, int lane, int mrow0,
-                                         int ncol0, const GemmDesc& d) {
+                                         int ncol0, const GemmDesc& d, const F& f = F()) {
     constexpr int ROWB = C::WN * (int)sizeof(TC);            // bytes per output row of the wave tile
     constexpr int PITCH = ROWB + 16;
     constexpr int RPP = staged_rows<C::WM, PITCH, WAVE_BYTES>(); // rows per pass
@@ -342,7 +347,7 @@ __device__ inline void write_tile_staged(const Acc (&acc)[C::FM][C::FN], char* l
             for (int j = 0; j < C::FN; ++j) {
                 vec_t v;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = cvt_out<TC>(acc[i][j][q]);
+                for (int q = 0; q < 4; ++q) v[q] = cvt_out<TC>(f(acc[i][j][q], j, q));
                 *reinterpret_cast<vec_t*>(rowp + j * 16 * sizeof(TC)) = v;
             }
         }
@@ -433,8 +438,14 @@ __device__ inline void write_tile_staged_epi(const f32x4 (&acc)[C::FM][C::FN], c
 #pragma unroll
                 for (int q = 0; q < 4; ++q) v[q] += bias_elem(row, col + q);
             }
+            // One uniform branch per chunk, not one per value.
+            if (logistic) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] = logistic ? act_logistic(v[q], k) : act_simple(v[q], d.act);
+                for (int q = 0; q < 4; ++q) v[q] = act_logistic(v[q], k);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = act_simple(v[q], d.act);
+            }
             if (row >= d.M) continue;
             TC* dst = reinterpret_cast<TC*>(Cb) + (int64_t)row * d.sc_m + col;
             if (vec_ok && col + 4 <= d.N) {
@@ -457,6 +468,41 @@ __device__ inline void write_tile_staged_epi(const f32x4 (&acc)[C::FM][C::FN], c
         }
     }
 }
+
+// Fused epilogue applied while the accumulators are staged (write_tile_staged's transform), for a
+// bias without a row stride or no bias: acc[i][j][q] is tile row 16i + lane%16, column
+// 16j + 4*(lane/16) + q, so the lane's FN x 4 bias values serve every row it holds.  16-bit outputs
+// then stage half the LDS bytes of the fp32 staging in write_tile_staged_epi, in half the passes.
+// LOGISTIC selects the activation family at compile time, so no value carries a branch.
+template <int FN, bool LOGISTIC>
+struct ColBiasAct {
+    float cb[FN][4];
+    ActCoef k;
+    int act;
+    __device__ ColBiasAct(const GemmDesc& d, int b, int ncol0, int lane) : k(act_coef(d.act)), act(d.act) {
+        if (d.bias != nullptr) {
+            const __amdgpu_buffer_rsrc_t br = make_rsrc(static_cast<const char*>(d.bias), d.bias_bytes);
+            const int64_t base = (int64_t)b * d.sbias_b;
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int col = ncol0 + 16 * j + 4 * (lane >> 4) + q;
+                    const unsigned bi = col < d.N ? (unsigned)(base + (int64_t)col * d.sbias_n) : kOOB;
+                    cb[j][q] = d.dtype_c == TV_FLOAT32 ? bias_load32(br, bi) : bias_load16(br, bi, d.dtype_c == TV_BFLOAT16);
+                }
+        } else {
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) cb[j][q] = 0.0f;
+        }
+    }
+    __device__ float operator()(float v, int j, int q) const {
+        v += cb[j][q];
+        return LOGISTIC ? act_logistic(v, k) : act_simple(v, act);
+    }
+};
 
 // Scheduling hints for the interleaved phases (LLVM AMDGPU sched_group_barrier masks).
 constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200, SG_VALU = 0x002;

@@ -53,22 +53,26 @@ __device__ inline bool has_epilogue(const GemmDesc& d) { return d.bias != nullpt
 // The reference's activations on float values (src/backend/cpu/activate.cpp:8-40,
 // src/backend/cuda/activate.cu:8-36): relu x > 0 ? x : 0, silu x / (1 + exp(-x)),
 // sigmoid 1 / (1 + exp(-x)), tanh(x).  The three logistic ones are one formula,
-// (a*x + c) * s + e with s = 1 / (1 + exp(-g*x)):
+// (a*x + c) * s + e with s = 1 / (1 + 2^(l*x)) and l = -g * log2(e):
 //   silu    a = 1, c = 0, e = 0,  g = 1
 //   sigmoid a = 0, c = 1, e = 0,  g = 1
 //   tanh    a = 0, c = 2, e = -1, g = 2      (tanh x = 2 / (1 + exp(-2x)) - 1)
-// evaluated with the hardware's approximate exp2 and reciprocal (__expf, __fdividef): a few ulp
-// relative for silu / sigmoid, about 1e-7 absolute for tanh near 0.
+// evaluated with the hardware's exp2 and reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each):
+// a few ulp relative for silu / sigmoid, about 1e-7 absolute for tanh near 0.  (__fdividef and
+// the / operator compile to the full IEEE division sequence here, about 11 instructions per value,
+// which made the activation the largest part of a fused epilogue.)
 struct ActCoef {
-    float a, c, e, g;
+    float a, c, e, l;
 };
 __host__ __device__ inline ActCoef act_coef(int act) {
-    if (act == TV_ACT_SIGMOID) return ActCoef{0.0f, 1.0f, 0.0f, 1.0f};
-    if (act == TV_ACT_TANH) return ActCoef{0.0f, 2.0f, -1.0f, 2.0f};
-    return ActCoef{1.0f, 0.0f, 0.0f, 1.0f}; // silu
+    constexpr float kLog2e = 1.4426950408889634f;
+    if (act == TV_ACT_SIGMOID) return ActCoef{0.0f, 1.0f, 0.0f, -kLog2e};
+    if (act == TV_ACT_TANH) return ActCoef{0.0f, 2.0f, -1.0f, -2.0f * kLog2e};
+    return ActCoef{1.0f, 0.0f, 0.0f, -kLog2e}; // silu
 }
 __device__ inline float act_logistic(float x, const ActCoef& k) {
-    const float s = __fdividef(1.0f, 1.0f + __expf(-k.g * x));
+    // 2^(l*x) overflows to +inf for large -x: s = rcp(inf) = 0, the limit.
+    const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(k.l * x));
     return (k.a * x + k.c) * s + k.e;
 }
 __device__ inline float act_simple(float x, int act) { return act == TV_ACT_RELU ? (x > 0.0f ? x : 0.0f) : x; }
