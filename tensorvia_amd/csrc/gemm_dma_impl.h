@@ -274,6 +274,50 @@ struct DmaOperand {
     static constexpr int kFragReads = MODE == LOAD_MNCONTIG ? 2 : 1;
 };
 
+// int8 output of a whole BM x BN tile.  A wave's own block is 64-byte rows (half a cache line), so
+// the per-wave staged store writes half lines; staged through LDS as one tile (rows padded by 16
+// bytes), every wave instead stores whole rows of the tile, 16 bytes per lane, with the streaming
+// policy.  The low byte of each exact int32 sum is kept (as the per-wave store does).  Entered with
+// the k-loop's LDS free (after a workgroup barrier); L holds at least BM * (BN + 16) bytes.
+template <class C>
+__device__ inline void write_tile_wg_i8(const i32x4 (&acc)[C::FM][C::FN], char* L, char* Cb, int lane, int wave, int wm,
+                                        int wn, int m0, int n0, const GemmDesc& d) {
+    constexpr int PITCH = C::BN + 16;
+    constexpr int NWAVES = C::THREADS / 64;
+    constexpr int CPR = C::BN / 16;               // 16-byte chunks per tile row
+    constexpr int RPW = C::BM / NWAVES;           // tile rows each wave stores
+    static_assert((RPW * CPR) % 64 == 0, "whole wave stores per row group");
+    // accumulators -> LDS: acc[i][j][q] is tile row wm*WM + 16i + lane%16, column
+    // wn*WN + 16j + 4*(lane/16) + q; the 4 bytes of one (i, j) are one dword.
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) {
+            const int r = wm * C::WM + 16 * i + (lane & 15);
+            const int c = wn * C::WN + 16 * j + 4 * (lane >> 4);
+            unsigned w = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) w |= (unsigned)(uint8_t)cvt_out<int8_t>(acc[i][j][q]) << (8 * q);
+            *reinterpret_cast<unsigned*>(L + r * PITCH + c) = w;
+        }
+    lds_barrier();
+#pragma unroll
+    for (int it = 0; it < RPW * CPR / 64; ++it) {
+        const int idx = it * 64 + lane;
+        const int r = wave * RPW + idx / CPR, c = idx % CPR;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(L + r * PITCH + c * 16);
+        const int row = m0 + r, col = n0 + c * 16;
+        if (row >= d.M) continue;
+        int8_t* dst = reinterpret_cast<int8_t*>(Cb) + (int64_t)row * d.sc_m + col;
+        if (col + 16 <= d.N) {
+            store_stream16(dst, v);
+        } else {
+            const int8_t* e = reinterpret_cast<const int8_t*>(&v);
+            for (int q = 0; q < 16 && col + q < d.N; ++q) dst[q] = e[q];
+        }
+    }
+}
+
 template <class C, bool FUSED = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
                           amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
@@ -453,7 +497,8 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
         char* lw = (wave < NWAVES / 2 ? S0 : S1) + (wave % (NWAVES / 2)) * EPI;
         const int mrow0 = m0 + wm * C::WM, ncol0 = n0 + wn * C::WN;
         if constexpr (__is_same(Acc, i32x4)) {
-            if (d.dtype_c == TV_INT8) write_tile_staged<int8_t, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d);
+            static_assert(C::BM * (C::BN + 16) <= 2 * STAGE, "the int8 tile staging fits the k-loop's LDS");
+            if (d.dtype_c == TV_INT8) write_tile_wg_i8<C>(acc, L, Cb, lane, wave, wm, wn, m0, n0, d);
             else write_tile_staged<int32_t, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d);
         } else {
             if (d.dtype_c == TV_BFLOAT16) write_tile_staged<__bf16, C, Acc, EPI>(acc, lw, Cb, lane, mrow0, ncol0, d);
