@@ -41,13 +41,14 @@ def to_f64(x, dt):
     return x.astype(np.float64)
 
 
-def run_case(dt_in, dt_out, batch, M, K, N, bias_kind, act, bt=False, seed=0, check=None):
-    """`check`: the batches compared against the fp64 reference (default: all)."""
+def run_case(dt_in, dt_out, batch, M, K, N, bias_kind, act, bt=False, seed=0, check=None, pad=0):
+    """`check`: the batches compared against the fp64 reference (default: all).  `pad` > 0: C is the
+    first N columns of rows N + pad long, and the padding must come back untouched."""
     import torch
     lead = (batch,) if batch else ()
     a = rng.make("uniform", lead + (M, K), 100 + seed, NAME[dt_in], -1, 1)
     b = rng.make("uniform", lead + ((N, K) if bt else (K, N)), 200 + seed, NAME[dt_in], -1, 1)
-    bshape = {"col": (N,), "full": lead + (M, N), "bcast": (M, N), "none": None}[bias_kind]
+    bshape = {"col": (N,), "colb": lead + (1, N), "full": lead + (M, N), "bcast": (M, N), "none": None}[bias_kind]
     bias = None if bshape is None else rng.make("uniform", bshape, 300 + seed, NAME[dt_out], -2, 2)
 
     ta = storage_to_torch(a, dt_in)
@@ -55,7 +56,8 @@ def run_case(dt_in, dt_out, batch, M, K, N, bias_kind, act, bt=False, seed=0, ch
     if bt:
         tb = tb.transpose(-1, -2)
     out_torch_dtype = {tv.FLOAT32: torch.float32, tv.BFLOAT16: torch.bfloat16, tv.FLOAT16: torch.float16}[dt_out]
-    tc = torch.empty(lead + (M, N), dtype=out_torch_dtype, device="cuda")
+    big = torch.full(lead + (M, N + pad), 3.0, dtype=out_torch_dtype, device="cuda")
+    tc = big[..., :N]
     args = tv.make_args(ta, tb, tc)
     ep = tv.TvEpilogue()
     ep.act = act
@@ -65,6 +67,8 @@ def run_case(dt_in, dt_out, batch, M, K, N, bias_kind, act, bt=False, seed=0, ch
         ep.bias = tbias.data_ptr()
         if bias_kind == "col":
             ep.sbias_b, ep.sbias_m, ep.sbias_n = 0, 0, 1
+        elif bias_kind == "colb":  # one column bias per batch
+            ep.sbias_b, ep.sbias_m, ep.sbias_n = (N if batch else 0), 0, 1
         elif bias_kind == "full":
             ep.sbias_b, ep.sbias_m, ep.sbias_n = (M * N if batch else 0), N, 1
         else:  # one [M, N] bias for every batch
@@ -72,6 +76,8 @@ def run_case(dt_in, dt_out, batch, M, K, N, bias_kind, act, bt=False, seed=0, ch
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     tv.check(tv.lib().tv_hip_gemm_ex(ctypes.byref(args), ctypes.byref(ep), s))
     torch.cuda.synchronize()
+    if pad:
+        assert bool((big[..., N:] == 3.0).all()), "the fused store wrote past column N"
     c = to_f64(torch_to_storage(tc), dt_out)
 
     fa, fb = to_f64(a, dt_in), to_f64(b, dt_in)
@@ -106,6 +112,17 @@ def test_fp32_mfma_kernel(act, bias_kind):
 @pytest.mark.parametrize("bias_kind", ["col", "full", "bcast"])
 def test_bf16_direct_load_kernel(act, bias_kind):
     run_case(tv.BFLOAT16, tv.BFLOAT16, 2, 300, 256, 270, bias_kind, act, seed=1)
+
+
+@pytest.mark.parametrize("dt_in,dt_out", [(tv.BFLOAT16, tv.BFLOAT16), (tv.FLOAT16, tv.FLOAT16),
+                                          (tv.BFLOAT16, tv.FLOAT32)], ids=["bf16", "fp16", "bf16-fp32out"])
+@pytest.mark.parametrize("act", list(ACTS), ids=lambda a: ACT_NAMES[a])
+@pytest.mark.parametrize("bias_kind", ["col", "colb", "none"])
+def test_direct_load_column_bias_vector_rows(dt_in, dt_out, act, bias_kind):
+    """Rows of C in whole 16-byte chunks (N = 264, a multiple of 8, inside padded rows of 280): the
+    direct-load kernel applies a column bias (shared, or one per batch) and the activation while it
+    stages the plain output store.  Ragged tiles in M (300) and N (264); the padding stays as it was."""
+    run_case(dt_in, dt_out, 2, 300, 256, 264, bias_kind, act, seed=21, pad=16)
 
 
 @pytest.mark.parametrize("act", [tv.ACT_RELU, tv.ACT_SILU])

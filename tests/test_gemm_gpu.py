@@ -54,6 +54,25 @@ def test_int8_vs_oracle_bit_exact(hip, shape):
     np.testing.assert_array_equal(to_storage(c), orc.mul(a, INT8, b, INT8))
 
 
+@pytest.mark.parametrize("batch,M,K,N,pad", [(0, 300, 200, 272, 0), (0, 300, 200, 260, 28), (2, 270, 136, 500, 12)])
+def test_int8_tile_store_ragged_and_padded(hip, batch, M, K, N, pad):
+    """int8 output with 16-byte aligned rows leaves as whole 256-byte tile rows staged through LDS:
+    ragged tiles in M and N, N not a multiple of 16 inside rows padded to a multiple of 16 bytes
+    (the last chunk of a row is written byte by byte), batched outputs.  Bit-exact against the
+    oracle, and the padding bytes are not written."""
+    lead = (batch,) if batch else ()
+    a = ints(31, lead + (M, K), -128, 127, np.int8)
+    b = ints(32, (K, N), -128, 127, np.int8)
+    big = torch.full(lead + (M, N + pad), 77, dtype=torch.int8, device="cuda")
+    c = big[..., :N]
+    hip.gemm(to_torch(a, INT8), to_torch(b, INT8), out=c)
+    torch.cuda.synchronize()
+    want = np.stack([orc.mul(a[i], INT8, b, INT8) for i in range(batch)]) if batch else orc.mul(a, INT8, b, INT8)
+    np.testing.assert_array_equal(to_storage(c), want)
+    if pad:
+        assert bool((big[..., N:] == 77).all()), "the tile store wrote past column N"
+
+
 def test_int8_int32_output(hip):
     a = ints(3, (200, 333), -128, 127, np.int8)
     b = ints(4, (333, 150), -128, 127, np.int8)
