@@ -666,10 +666,13 @@ static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices, const Ge
     return hipGetLastError();
 }
 
-// The matrix-core GEMV (bf16 / fp16 with 64-column strips, int8 with 128-column strips): same
-// K-slice rule as gemv_run.
+// K slices of the matrix-core GEMV asked for as `nslices`: at least what x's LDS slice needs, rows
+// per slice a multiple of the 16-byte vector; S is what the rounding leaves.
+struct GemvSlices {
+    int S, kslice, kpad;
+};
 template <typename T, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
-static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices, const GemvScratch* fixed) {
+static GemvSlices gemv_mfma_slices(const GemmDesc& d, int nslices) {
     using Acc = typename GemvTraits<T>::Acc;
     constexpr int ES = sizeof(T), VEC = 16 / ES, NB = 8 * VEC, CH = 64 / ES;
     // A workgroup's LDS (at most 160 KB) holds the kernel's static arrays and x's rows of a slice:
@@ -679,8 +682,6 @@ static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices, con
     static_assert(kStatic + 8 * ES * CH <= kLds, "static LDS leaves no room for x");
     constexpr int kFit = (kLds - kStatic) / (8 * ES) / CH * CH;
     constexpr int KCAP = gemv_kcap<T>() < kFit ? gemv_kcap<T>() : kFit; // a multiple of CH
-    if (d.K < 1) return TV_E_UNSUPPORTED;
-    const int nblk = (d.N + NB - 1) / NB;
     int S = nslices < 1 ? 1 : nslices;
     const int min_s = (d.K + KCAP - 1) / KCAP;
     if (S < min_s) S = min_s;
@@ -688,6 +689,18 @@ static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices, con
     kslice = (kslice + VEC - 1) / VEC * VEC;
     if (kslice > KCAP) kslice = KCAP;
     S = (d.K + kslice - 1) / kslice;
+    return GemvSlices{S, kslice, (kslice + CH - 1) / CH * CH};
+}
+
+// The matrix-core GEMV (bf16 / fp16 with 64-column strips, int8 with 128-column strips).
+template <typename T, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
+static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices, const GemvScratch* fixed) {
+    using Acc = typename GemvTraits<T>::Acc;
+    constexpr int ES = sizeof(T), VEC = 16 / ES, NB = 8 * VEC;
+    if (d.K < 1) return TV_E_UNSUPPORTED;
+    const int nblk = (d.N + NB - 1) / NB;
+    const GemvSlices sl = gemv_mfma_slices<T, WAVES, DEPTH>(d, nslices);
+    const int S = sl.S, kslice = sl.kslice;
     if (S > kGemvMaxSlices) return TV_E_UNSUPPORTED;
     if ((int64_t)(kslice - 1) * d.sb_k * ES + (int64_t)d.N * ES >= ((int64_t)1 << 30)) return TV_E_UNSUPPORTED;
     const int64_t nwg = (int64_t)nblk * d.batch;
@@ -704,11 +717,32 @@ static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices, con
         const int rc = split_buffers(stream, fixed, nwg, (size_t)nwg * S * 8 * NB * sizeof(Acc), g);
         if (rc) return rc;
     }
-    const int kpad = (kslice + CH - 1) / CH * CH; // at most KCAP, a multiple of CH
-    hipLaunchKernelGGL((gemv_mfma_kernel<T, WAVES, DEPTH>), dim3((unsigned)nwg, S), dim3(WAVES * 64), (size_t)8 * kpad * ES, stream, g);
+    hipLaunchKernelGGL((gemv_mfma_kernel<T, WAVES, DEPTH>), dim3((unsigned)nwg, S), dim3(WAVES * 64), (size_t)8 * sl.kpad * ES, stream, g);
     return hipGetLastError();
 }
 
+// Workgroups of the matrix-core GEMV that the current device holds at once: resident workgroups
+// per CU at the launch's LDS size (the occupancy API) times the CUs.  Cached per device and LDS
+// size (x's slice is the only part that varies); 0 if the runtime cannot tell.
+template <typename T, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
+static int64_t gemv_mfma_capacity(int kpad) {
+    static std::mutex mu;
+    static std::map<std::pair<int, int>, int64_t> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lk(mu);
+    const auto key = std::make_pair(dev, kpad);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(gemv_mfma_kernel<T, WAVES, DEPTH>),
+                                                     WAVES * 64, (size_t)8 * kpad * sizeof(T)) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    const int64_t cap = (int64_t)(per_cu > 0 ? per_cu : 0) * (cus > 0 ? cus : 0);
+    cache[key] = cap;
+    return cap;
+}
 
 template <typename T, int MR>
 static int gemv_dispatch_nl(const GemmDesc& d, hipStream_t stream, const GemvPlan& p, const GemvScratch* fixed) {
@@ -753,23 +787,76 @@ int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads,
 // The matrix-core kernel serves 16-bit W at every M and int8 W at M >= 3, with whole 128-byte
 // strips (N >= 64 columns at 16 bits, N >= 128 at 8).  On c5's W shape, against the dot-product
 // kernel: bf16 18.7 / 19.3 / 20.2 us at M = 1 / 4 / 8 (dot 19.2 / 20.9 / 25.7); int8 13.7 us at
-// M = 8 (dot 20.5) but 12.1 us at M = 1 (dot 11.5).  Its slices: about 128 KB of W per workgroup
-// (688 workgroups in all at 16 bits, 344 in int8: 4 slices of c5's K, best among 1-16), at least
-// what x's LDS slice needs, and no more than leaves each wave two chunks per slice.
+// M = 8 (dot 20.5) but 12.1 us at M = 1 (dot 11.5).
+//
+// Slices: about 688 workgroups at 16 bits and 344 in int8 (4 slices of c5's W, the best of 1-16 at
+// every M), unless that count lands where a sweep of 1-16 slices over nine W shapes (bf16 M = 1
+// and 8, int8 M = 8; K 2048-14336, N 4096-32768) found launches slow:
+//  * workgroups / resident capacity in (1.0, 1.4): a second round that is mostly empty
+//    (W[4096, 14336]: 4 slices 27.9 us, 3 slices 24.5 us, 2 slices 23.7 us);
+//  * fewer resident workgroups per CU than the shape allows elsewhere, up to 3 (x's LDS slice of
+//    few, long slices leaves room for one: W[8192, 28672], 2 slices 119 us, 5 slices 81 us);
+//  * under 0.6 of a round.
+// It then takes the nearest slice count (more slices first) that avoids all three.  The resident
+// capacity comes from the occupancy API at the launch's LDS size.
+template <typename T>
+static int gemv_mfma_pick(const GemmDesc& d) {
+    constexpr int ES = sizeof(T), NB = 128 / ES, CH = 64 / ES;
+    const int64_t strips = (int64_t)(d.N + NB - 1) / NB * d.batch;
+    int max_s = d.K / (8 * CH) > 1 ? d.K / (8 * CH) : 1; // each wave at least two chunks per slice
+    if (max_s > kGemvMaxSlices) max_s = kGemvMaxSlices;
+    const int64_t target = ES == 2 ? 688 : 344;
+    int s0 = (int)((target + strips - 1) / strips);
+    if (s0 > max_s) s0 = max_s;
+    s0 = gemv_mfma_slices<T>(d, s0).S; // raised to what x's LDS slice needs
+
+    static std::mutex mu;
+    static std::map<std::tuple<int, int64_t, int>, int> picked; // (device, strips, K) -> S
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return s0;
+    const auto key = std::make_tuple(dev, strips, d.K);
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        const auto it = picked.find(key);
+        if (it != picked.end()) return it->second;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return s0;
+    const int top = s0 > max_s ? s0 : max_s;
+    int64_t cap[kGemvMaxSlices + 2] = {};
+    int s_of[kGemvMaxSlices + 2] = {};
+    int occ_best = 0;
+    for (int s = 1; s <= top && s <= kGemvMaxSlices; ++s) {
+        const GemvSlices sl = gemv_mfma_slices<T>(d, s);
+        s_of[s] = sl.S;
+        cap[s] = gemv_mfma_capacity<T>(sl.kpad);
+        if (cap[s] <= 0) return s0;
+        const int occ = (int)(cap[s] / cus);
+        if (occ > occ_best) occ_best = occ;
+    }
+    const int occ_req = occ_best < 3 ? occ_best : 3;
+    auto good = [&](int s) {
+        if (s < 1 || s > top || s > kGemvMaxSlices || s_of[s] != s) return false;
+        const double r = (double)(strips * s) / (double)cap[s];
+        return cap[s] / cus >= occ_req && r >= 0.6 && !(r > 1.0 && r < 1.4);
+    };
+    int S = s0;
+    if (!good(s0)) {
+        for (int dist = 1; dist <= kGemvMaxSlices; ++dist) {
+            if (good(s0 + dist)) { S = s0 + dist; break; }
+            if (good(s0 - dist)) { S = s0 - dist; break; }
+        }
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    picked[key] = S;
+    return S;
+}
+
 static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed) {
-    const int es = (int)dtype_size(d.dtype_a);
-    const int nb = 128 / es, ch = 64 / es;
-    const int64_t strips = (int64_t)(d.N + nb - 1) / nb * d.batch;
-    const int max_s = d.K / (8 * ch) > 1 ? d.K / (8 * ch) : 1;
-    const int64_t target = es == 2 ? 688 : 344;
-    int s = (int)((target + strips - 1) / strips);
-    if (s > max_s) s = max_s;
-    if (s > kGemvMaxSlices) s = kGemvMaxSlices;
-    // gemv_mfma_run raises s to what x's LDS slice needs
     switch (d.dtype_a) {
-        case TV_BFLOAT16: return gemv_mfma_run<__bf16>(d, stream, s, fixed);
-        case TV_FLOAT16: return gemv_mfma_run<_Float16>(d, stream, s, fixed);
-        default: return gemv_mfma_run<int8_t>(d, stream, s, fixed);
+        case TV_BFLOAT16: return gemv_mfma_run<__bf16>(d, stream, gemv_mfma_pick<__bf16>(d), fixed);
+        case TV_FLOAT16: return gemv_mfma_run<_Float16>(d, stream, gemv_mfma_pick<_Float16>(d), fixed);
+        default: return gemv_mfma_run<int8_t>(d, stream, gemv_mfma_pick<int8_t>(d), fixed);
     }
 }
 

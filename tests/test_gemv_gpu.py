@@ -55,6 +55,25 @@ def test_gemv_integer_inputs_exact(hip, dt, M, KN):
     np.testing.assert_array_equal(c, want)
 
 
+@pytest.mark.parametrize("dt,M,K,N", [(BFLOAT16, 1, 4096, 14336), (BFLOAT16, 8, 8192, 28672), (INT8, 8, 8192, 28672),
+                                      (BFLOAT16, 1, 2048, 32768)])
+def test_gemv_large_w_slice_choice_exact(hip, dt, M, K, N):
+    """W shapes whose K-slice count comes from the occupancy rule rather than the 688 / 344
+    workgroup target (224, 448 and 512 strips): integer-valued inputs, exact sums, bit-exact
+    against exact integer sums (fp32 output for bf16: |sum| <= 4K < 2^24)."""
+    if dt == INT8:
+        x = rng.uniform_int(40, M * K, -128, 127).astype(np.int8).reshape(M, K)
+        w = rng.uniform_int(41, K * N, -128, 127).astype(np.int8).reshape(K, N)
+        c32 = hip.gemv(to_torch(x, INT8), to_torch(w, INT8), out_dtype=INT32)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_storage(c32), orc.exact_int(x, w).astype(np.int32))
+        return
+    x = rng.uniform_int(42, M * K, -2, 2).astype(np.float32).reshape(M, K)
+    w = rng.uniform_int(43, K * N, -2, 2).astype(np.float32).reshape(K, N)
+    c = to_storage(hip.gemv(to_torch(half_bits(x, dt), dt), to_torch(half_bits(w, dt), dt), out_dtype=FLOAT32))
+    np.testing.assert_array_equal(c, (x.astype(np.float64) @ w.astype(np.float64)).astype(np.float32))
+
+
 @pytest.mark.parametrize("dt", [BFLOAT16, FLOAT32])
 def test_gemv_uniform_vs_oracle(hip, dt):
     M, K, N = 4, 2048, 3000
