@@ -7,7 +7,8 @@ BASELINE.json's configs[1], the config the bench contract quotes at N=1 (configs
 reference's README shape, which its own CPU backend runs).  The other configurations are measured
 in the same run and reported under ``configs``, each with its own CPU baseline.
 
-Timing: W untimed launches, then K back-to-back launches in 5 runs, with HIP events on the launch
+Timing: 40 ms of untimed launches of the configuration's own kernel (the GPU's clocks settle to
+the load), W untimed launches, then K back-to-back launches in 5 runs, with HIP events on the launch
 stream at the run boundaries: the mean over all K is the per-launch time the line reports and the
 roofline uses; the median of the 5 runs' per-launch means is reported beside it.  The CPU baseline
 is the oracle's restatement of MulImpl<CPU> (src/backend/cpu/mul.cpp:97-145) on the box's host
@@ -87,7 +88,7 @@ DESC = {
 DTYPE = {"c1": "fp32", "c2": "int8", "c3": "bf16", "c3_fused": "bf16", "c4": "fp16", "c5m1": "bf16", "c5m8": "bf16"}
 # The kernel each configuration's launch runs.
 KERNEL = {
-    "c1": "gemm_mfma_kernel<GemmCfg<float, 128, 128, 2, 2, 0, 1>, false>",
+    "c1": "gemm_mfma_sk_kernel<GemmCfg<float, 128, 128, 2, 2, 0, 1>, false> (stream-K schedule)",
     "c2": "gemm_dma_kernel<GemmCfg<signed char, 256, 256, 2, 4, 0, 1>, false>",
     "c3": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, false>",
     "c3_fused": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, true>",
@@ -116,14 +117,28 @@ def work(name: str, inp) -> tuple[float, float]:
     return 2.0 * B * M * N * K, (a.size + b.size) * es + B * M * N * es
 
 
+# Untimed running time of each configuration's own launches before its W warm-up launches.  The
+# GPU's clocks follow the load: on MI355X, c1's first blocks of 20 launches ran 428, 386, 366 and
+# then 350 us (about 25 ms to settle, fresh or reused buffers alike), and a global warm-up with
+# another kernel did not settle them for the next one.
+SETTLE_S = 0.04
+
+
 def timed_launches(launch, steps: int, warmup: int, stream, groups: int = 5):
-    """W untimed launches, then K back-to-back launches in `groups` runs of consecutive launches,
-    with a HIP event on the launch stream at each run boundary.  Returns the mean per-launch time
-    over the whole timed region, the median over the runs of their per-launch means, and the host
-    wall time per step."""
+    """SETTLE_S of untimed launches and W untimed launches, then K back-to-back launches in `groups`
+    runs of consecutive launches, with a HIP event on the launch stream at each run boundary.
+    Returns the mean per-launch time over the whole timed region, the median over the runs of
+    their per-launch means, and the host wall time per step."""
     import torch
+    t_settle = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t_settle < SETTLE_S:
+        for _ in range(4):
+            launch(n)
+            n += 1
+        torch.cuda.synchronize()
     for i in range(warmup):
-        launch(i)
+        launch(n + i)
     torch.cuda.synchronize()
     groups = max(1, min(groups, steps))
     bounds = [round(g * steps / groups) for g in range(groups + 1)]
@@ -480,6 +495,7 @@ def main() -> int:
         "data": "synthetic: seeded counter-based generator (SplitMix64), uniform ints in [-10,10]",
         "config": {"workload": "c2: " + DESC["c2"], "M": 4096, "N": 4096, "K": 4096, "accumulate": "int32",
                    "why": "BASELINE.json configs[1], the single-GPU config the metric is quoted on"},
+        "settle_s_per_config": SETTLE_S,
         "roofline": roof,
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in (
             "value", "unit", "cores", "kind", "sample", "nproc", "omp_num_threads", "openmp_threads", "effective_threads")},

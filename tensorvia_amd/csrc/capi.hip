@@ -83,7 +83,8 @@ int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
 }
 
 // Routing shared by tv_hip_gemm, tv_hip_gemm_ex and tv_hip_gemm_noalloc (fixed: the GEMV's
-// split-K buffers, nullptr for the per-stream workspace).
+// split-K buffers, nullptr for the per-stream workspace; with fixed buffers the GEMM takes no
+// schedule that needs a workspace either).
 int run_gemm(const tv_gemm_args* args, const tvk::GemmDesc& d, hipStream_t s, const tvk::GemvScratch* fixed = nullptr) {
     if (d.batch == 0 || d.M == 0 || d.N == 0) return TV_OK;
     if (mfma_pair(args) && d.K == 0) return tvk::launch_gemm_k0(d, s);
@@ -92,7 +93,7 @@ int run_gemm(const tv_gemm_args* args, const tvk::GemmDesc& d, hipStream_t s, co
             const int rc = tvk::launch_gemv(d, s, fixed);
             if (rc != TV_E_UNSUPPORTED) return rc;
         }
-        return tvk::launch_gemm_mfma(d, s);
+        return tvk::launch_gemm_mfma(d, s, fixed == nullptr);
     }
     return tvk::launch_gemm_simt(d, s);
 }

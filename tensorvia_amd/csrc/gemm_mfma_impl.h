@@ -517,40 +517,18 @@ __device__ inline void lds_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <class C, bool FUSED = false>
-__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
-                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
-void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec) {
+// The k-loop of one output tile over k-tiles [kt0, kt1), accumulating into acc (the caller zeroes
+// it).  b, m0, n0: the tile's batch and origin.
+template <class C>
+__device__ inline void mfma_tile_kloop(const GemmDesc& d, char* smem, int b, int m0, int n0, int kt0, int kt1,
+                                       typename Mfma<typename C::T>::Acc (&acc)[C::FM][C::FN]) {
     using T = typename C::T;
     using Op = Mfma<T>;
-    using Acc = typename Op::Acc;
     constexpr int ES = C::ES;
-
-    constexpr int SMEM = 2 * C::STAGE > kEpiWaveBytes * C::THREADS / 64 ? 2 * C::STAGE : kEpiWaveBytes * C::THREADS / 64;
-    __shared__ __attribute__((aligned(16))) char smem[SMEM];
-
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
-
-    // Workgroup -> tile.  The hardware deals workgroup ids round-robin over the 8 XCDs; undo that
-    // so that a contiguous range of logical tiles lands on one XCD, then walk tiles in groups of
-    // `group_m` tile-rows so neighbouring workgroups share A rows and B columns in that XCD's L2.
-    int bid = blockIdx.x;
-    const int nwg = gridDim.x;
-    if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
-    const int per_batch = tiles_m * tiles_n;
-    const int b = bid / per_batch;
-    int r = bid - b * per_batch;
-    const int span = group_m * tiles_n;
-    const int g = r / span;
-    const int first_m = g * group_m;
-    const int gsz = min(tiles_m - first_m, group_m);
-    r -= g * span;
-    const int tm = first_m + r % gsz;
-    const int tn = r / gsz;
-    const int m0 = tm * C::BM, n0 = tn * C::BN;
 
     TileLoader<C::AMODE, C::BM, C::THREADS, ES> la;
     la.base = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + (int64_t)m0 * d.sa_m) * ES;
@@ -558,12 +536,6 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
     TileLoader<C::BMODE, C::BN, C::THREADS, ES> lb;
     lb.base = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)n0 * d.sb_n) * ES;
     lb.s_r = d.sb_n; lb.s_k = d.sb_k; lb.rows_valid = d.N - n0; lb.K = d.K;
-
-    Acc acc[C::FM][C::FN];
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
 
     u32x4 ra[decltype(la)::NCH];
     u32x4 rb[decltype(lb)::NCH];
@@ -592,14 +564,13 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
         }
     };
 
-    const int nk = (d.K + C::BK - 1) / C::BK;
-    // Prologue: tile 0 -> LDS stage 0, tile 1 -> registers, k-group 0 fragments of tile 0.
-    la.load(tid, 0, ra);
-    lb.load(tid, 0, rb);
+    // Prologue: k-tile kt0 -> LDS stage 0, kt0 + 1 -> registers, k-group 0 fragments of kt0.
+    la.load(tid, kt0 * C::BK, ra);
+    lb.load(tid, kt0 * C::BK, rb);
     la.store(tid, smem, ra);
     lb.store(tid, smem + C::A_BYTES, rb);
-    la.load(tid, C::BK, ra);
-    lb.load(tid, C::BK, rb);
+    la.load(tid, (kt0 + 1) * C::BK, ra);
+    lb.load(tid, (kt0 + 1) * C::BK, rb);
     lds_barrier();
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) fb[j] = b_frag(smem, 0, j);
@@ -610,9 +581,10 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
     constexpr int NRD = C::FM * decltype(la)::kFragReads + C::FN * decltype(lb)::kFragReads; // LDS reads per k-group
     constexpr int NLD = decltype(la)::NCH + decltype(lb)::NCH;        // buffer loads per tile
 
-    for (int kt = 0; kt < nk; ++kt) {
-        char* cur = smem + (kt & 1) * C::STAGE;
-        char* nxt = smem + ((kt + 1) & 1) * C::STAGE;
+    // k-tiles past kt1 are loaded ahead (zeros past K) but never multiplied.
+    for (int kt = kt0; kt < kt1; ++kt) {
+        char* cur = smem + ((kt - kt0) & 1) * C::STAGE;
+        char* nxt = smem + ((kt - kt0 + 1) & 1) * C::STAGE;
         // Phase A: tile kt+1 -> LDS, tile kt+2 -> registers, MFMAs of k-group 0 of tile kt
         // (reading k-group 1's fragments of tile kt on the way).
         const int t = opaque(tid);
@@ -655,10 +627,19 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
             __builtin_amdgcn_sched_group_barrier(SG_MFMA, NMF - NRD, 0);
         }
     }
-    (void)SG_VALU;
+}
 
-    // Epilogue.  acc[i][j][q] = C[m0 + wm*WM + 16i + lane%16][n0 + wn*WN + 16j + 4*(lane/16) + q].
-    // The output type is chosen once; each branch is straight-line code over the accumulators.
+// Epilogue of one output tile: acc[i][j][q] = C[m0 + wm*WM + 16i + lane%16][n0 + wn*WN + 16j +
+// 4*(lane/16) + q].  The output type is chosen once; each branch is straight-line code over the
+// accumulators.
+template <class C, bool FUSED>
+__device__ inline void mfma_tile_store(const GemmDesc& d, char* smem, int b, int m0, int n0, int c_vec,
+                                       const typename Mfma<typename C::T>::Acc (&acc)[C::FM][C::FN]) {
+    using Acc = typename Mfma<typename C::T>::Acc;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
     const size_t csz = dtype_size(d.dtype_c);
     char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
     const int row0 = m0 + wm * C::WM + (lane & 15);
@@ -699,6 +680,137 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
     }
 }
 
+// Workgroup id -> (batch, tile row, tile column).  The hardware deals workgroup ids round-robin over
+// the 8 XCDs; the id is first remapped so that a contiguous range of logical tiles lands on one XCD,
+// then tiles are walked in groups of `group_m` tile-rows so that neighbouring workgroups share A rows
+// and B columns in that XCD's L2.
+__device__ inline void mfma_tile_of(int lin, int tiles_m, int tiles_n, int group_m, int& b, int& tm, int& tn) {
+    const int per_batch = tiles_m * tiles_n;
+    b = lin / per_batch;
+    int r = lin - b * per_batch;
+    const int span = group_m * tiles_n;
+    const int g = r / span;
+    const int first_m = g * group_m;
+    const int gsz = min(tiles_m - first_m, group_m);
+    r -= g * span;
+    tm = first_m + r % gsz;
+    tn = r / gsz;
+}
+
+template <class C, bool FUSED = false>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
+                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
+void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec) {
+    using Acc = typename Mfma<typename C::T>::Acc;
+    constexpr int SMEM = 2 * C::STAGE > kEpiWaveBytes * C::THREADS / 64 ? 2 * C::STAGE : kEpiWaveBytes * C::THREADS / 64;
+    __shared__ __attribute__((aligned(16))) char smem[SMEM];
+
+    int bid = blockIdx.x;
+    const int nwg = gridDim.x;
+    if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+    int b, tm, tn;
+    mfma_tile_of(bid, tiles_m, tiles_n, group_m, b, tm, tn);
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
+
+    Acc acc[C::FM][C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+    mfma_tile_kloop<C>(d, smem, b, m0, n0, 0, (d.K + C::BK - 1) / C::BK, acc);
+    mfma_tile_store<C, FUSED>(d, smem, b, m0, n0, c_vec, acc);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Stream-K schedule (fp32): G resident workgroups take equal contiguous ranges of the (tile, k-tile)
+// iteration space instead of one workgroup per tile.  Every CU then does the same work however the
+// tiles divide over the CUs (c1: 672 tiles of 128x128 on 256 CUs, 2.625 per CU, which the
+// one-per-tile launch runs in the time of 3), and fewer tiles than CUs still use every CU.  Workgroup w owns iterations
+// [w*I/G, (w+1)*I/G); a tile cut by a range boundary is computed in segments by consecutive
+// workgroups.  Each segment stores its accumulators in a slot (register order, 16 bytes a lane),
+// counts itself in (publish_and_count), and the last segment to arrive sums the slots in segment
+// order (deterministic) and writes the tile.  Workgroup w's slots: 2w for the segment that continues
+// a tile begun before its range, 2w + 1 for the one that begins a tile that runs past it (a range
+// holds at most one of each).  No workgroup waits for another.
+struct SkArgs {
+    int64_t iters; // tiles x k-tiles
+    int nk;        // k-tiles per tile
+    int* cnt;      // [tiles] arrival counters, zero between launches
+    char* slots;   // [2 x workgroups][slot bytes]
+};
+
+template <class C> constexpr int sk_slot_bytes() { return C::THREADS / 64 * C::FM * C::FN * 64 * 16; }
+
+template <class C, bool FUSED = false>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
+                          amdgpu_waves_per_eu(2 * C::THREADS / 256, 2 * C::THREADS / 256))) // 2 per CU, as the plain kernel
+void gemm_mfma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec, SkArgs sk) {
+    using Acc = typename Mfma<typename C::T>::Acc;
+    static_assert(__is_same(Acc, f32x4), "stream-K slots hold fp32 accumulators");
+    constexpr int SMEM = 2 * C::STAGE > kEpiWaveBytes * C::THREADS / 64 ? 2 * C::STAGE : kEpiWaveBytes * C::THREADS / 64;
+    constexpr int SLOT = sk_slot_bytes<C>();
+    __shared__ __attribute__((aligned(16))) char smem[SMEM];
+    __shared__ int last_flag;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = gridDim.x;
+    int w = blockIdx.x;
+    if ((G & 7) == 0) w = (w & 7) * (G >> 3) + (w >> 3); // consecutive ranges on one XCD
+    const int64_t I = sk.iters;
+    const int nk = sk.nk;
+    const int64_t it_end = (int64_t)(w + 1) * I / G;
+    // The workgroup whose range holds iteration it: the largest v with floor(v * I / G) <= it.
+    auto owner = [&](int64_t it) { return (int)(((it + 1) * G - 1) / I); };
+    auto slot_rsrc = [&](int slot) { return make_rsrc(sk.slots + (int64_t)slot * SLOT, SLOT); };
+
+    for (int64_t it = (int64_t)w * I / G; it < it_end;) {
+        const int tile = (int)(it / nk);
+        const int kt0 = (int)(it - (int64_t)tile * nk);
+        const int kt1 = (int)min((int64_t)nk, kt0 + (it_end - it));
+        it += kt1 - kt0;
+        int b, tm, tn;
+        mfma_tile_of(tile, tiles_m, tiles_n, group_m, b, tm, tn);
+        const int m0 = tm * C::BM, n0 = tn * C::BN;
+        Acc acc[C::FM][C::FN];
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+        lds_barrier(); // the previous segment's epilogue is done with the LDS
+        mfma_tile_kloop<C>(d, smem, b, m0, n0, kt0, kt1, acc);
+        if (kt0 != 0 || kt1 != nk) {
+            const int64_t t0 = (int64_t)tile * nk;
+            const int first = owner(t0), last = owner(t0 + nk - 1);
+            {
+                const __amdgpu_buffer_rsrc_t r = slot_rsrc(w == first ? 2 * w + 1 : 2 * w);
+#pragma unroll
+                for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < C::FN; ++j)
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[i][j]), r,
+                                                               (((wave * C::FM + i) * C::FN + j) * 64 + lane) * 16, 0, 16);
+            }
+            publish_and_count(sk.cnt + tile, last - first + 1, &last_flag);
+            if (!last_flag) continue;
+            // Sum the segments' slots in segment order (this workgroup's own included).
+            for (int v = first; v <= last; ++v) {
+                const __amdgpu_buffer_rsrc_t r = slot_rsrc(v == first ? 2 * v + 1 : 2 * v);
+#pragma unroll
+                for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < C::FN; ++j) {
+                        const f32x4 p = __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (((wave * C::FM + i) * C::FN + j) * 64 + lane) * 16, 0, 16));
+                        acc[i][j] = v == first ? p : acc[i][j] + p;
+                    }
+            }
+            if (threadIdx.x == 0) __hip_atomic_store(sk.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        mfma_tile_store<C, FUSED>(d, smem, b, m0, n0, c_vec, acc);
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Host side: pick the operand load modes and the tile configuration.
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -722,8 +834,48 @@ static int pick_mode(const void* p, int64_t R, int64_t K, int64_t s_r, int64_t s
     return LOAD_GENERIC;
 }
 
+// Workgroups of the stream-K kernel resident at once on the current device (occupancy API x CUs),
+// cached per device; 0 if the runtime cannot tell.
 template <class C>
-static int run_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
+static int sk_grid() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cached[dev] > 0) return cached[dev];
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(gemm_mfma_sk_kernel<C, false>), C::THREADS, 0) !=
+            hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
+        return 0;
+    cached[dev] = per_cu * cus;
+    return cached[dev];
+}
+
+// The stream-K launch: K of at least 8 k-tiles, at least 8 k-tiles per workgroup.  Measured against
+// one workgroup per tile with random fp32 inputs (same box): c1 [2592,2048]@[2048,4096] 350-366
+// against 418-453 us; 512 / 768 / 1024 tiles of 128x128 (K 2048-4096) 11-13 % faster; [1024]^3
+// 37.1 against 70.9 us.  Returns 1 if it did not launch.
+template <class C, bool FUSED>
+static int run_cfg_sk(const GemmDesc& d, hipStream_t stream, int group_m, int tiles_m, int tiles_n, int64_t ntiles, int c_vec) {
+    const int nk = (d.K + C::BK - 1) / C::BK;
+    if (nk < 8) return 1;
+    int G = sk_grid<C>();
+    if (G <= 0) return 1;
+    const int64_t iters = ntiles * nk;
+    if (iters / 8 < G) G = (int)(iters / 8);
+    if (G < 1) return 1;
+    SkArgs sk;
+    sk.iters = iters;
+    sk.nk = nk;
+    const int rc = gemm_sk_workspace(stream, (size_t)ntiles, (size_t)2 * G * sk_slot_bytes<C>(), &sk.cnt, &sk.slots);
+    if (rc) return rc;
+    hipLaunchKernelGGL((gemm_mfma_sk_kernel<C, FUSED>), dim3((unsigned)G), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
+                       group_m, c_vec, sk);
+    return hipGetLastError();
+}
+
+template <class C>
+static int run_cfg(const GemmDesc& d, hipStream_t stream, int group_m, bool may_alloc = true) {
     const int tiles_m = (d.M + C::BM - 1) / C::BM;
     const int tiles_n = (d.N + C::BN - 1) / C::BN;
     const int64_t nwg = (int64_t)tiles_m * tiles_n * d.batch;
@@ -741,6 +893,12 @@ static int run_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
     // The fused epilogue runs in the staged store only (16-byte aligned rows of C).
     const bool epi = d.bias != nullptr || d.act != TV_ACT_NONE;
     if (epi && d.sc_n != 1) return TV_E_UNSUPPORTED; // the fused store writes rows of C
+    if constexpr (__is_same(typename C::T, float))
+        if (may_alloc) {
+            const int rc = epi ? run_cfg_sk<C, true>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec)
+                               : run_cfg_sk<C, false>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec);
+            if (rc != 1) return rc;
+        }
     if constexpr (!__is_same(typename C::T, int8_t))
         if (epi) {
             hipLaunchKernelGGL((gemm_mfma_kernel<C, true>), dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
@@ -755,12 +913,12 @@ static int run_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
 // Tile shapes: the large tile serves the vector load modes; any operand that needs element
 // gathers runs a 128x128 tile (fewer registers, faster to build, rarely used).
 template <typename T, int BM, int BN, int WMW, int WNW>
-static int run_modes(const GemmDesc& d, hipStream_t stream, int group_m) {
+static int run_modes(const GemmDesc& d, hipStream_t stream, int group_m, bool may_alloc = true) {
     const int es = (int)sizeof(T);
     const int am = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, BM);
     const int bm = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, BN);
 #define TV_CASE(A_, B_) \
-    if (am == A_ && bm == B_) return run_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream, group_m);
+    if (am == A_ && bm == B_) return run_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream, group_m, may_alloc);
     TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)
     TV_CASE(LOAD_KCONTIG, LOAD_KCONTIG)
     TV_CASE(LOAD_MNCONTIG, LOAD_MNCONTIG)
@@ -770,7 +928,7 @@ static int run_modes(const GemmDesc& d, hipStream_t stream, int group_m) {
     const int am2 = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, 128);
     const int bm2 = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, 128);
 #define TV_CASE(A_, B_) \
-    if (am2 == A_ && bm2 == B_) return run_cfg<GemmCfg<T, 128, 128, 2, 2, A_, B_>>(d, stream, group_m);
+    if (am2 == A_ && bm2 == B_) return run_cfg<GemmCfg<T, 128, 128, 2, 2, A_, B_>>(d, stream, group_m, may_alloc);
     TV_CASE(LOAD_KCONTIG, LOAD_GENERIC)
     TV_CASE(LOAD_MNCONTIG, LOAD_GENERIC)
     TV_CASE(LOAD_GENERIC, LOAD_MNCONTIG)

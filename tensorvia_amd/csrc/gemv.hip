@@ -154,30 +154,6 @@ __device__ inline int xcd_remap(int bid, int nwg) {
     return (nwg & 7) == 0 ? (bid & 7) * (nwg >> 3) + (bid >> 3) : bid;
 }
 
-// Split-K hand-over between the workgroups of one strip.  Called by every thread after its
-// partial-slot stores, which are agent-scope atomic stores (global_store ... sc1: written through
-// the XCD's L2 to the agent's coherence point, never left dirty in an L2).
-//  * Each wave waits until its own slot stores are acknowledged (s_waitcnt vmcnt(0); for a store
-//    the count drops when the write is complete at the scope it was issued with).  The asm's
-//    memory clobber keeps the compiler from moving the stores below the wait.
-//  * After the barrier every slot store of the workgroup is complete; thread 0 then counts the
-//    workgroup in with an agent-scope atomic add, so a count that completes the strip is taken
-//    after every publisher's stores are complete.
-//  * The combining workgroup reads the slots with agent-scope atomic loads (sc1), which are
-//    served from the coherence point, issued after the count returned (through the barrier).
-// This is the ordering-only release that rocPRIM's look-back scan uses on this architecture for
-// data published through agent-scope atomics: a C++ release/acquire fence pair at agent scope
-// also writes back and invalidates the XCD's whole L2 (buffer_wbl2 sc1, buffer_inv sc1) once per
-// wave, which measured 104 us on c5 (x[1,4096] @ W[4096,11008] bf16) against 18.5 us with this
-// hand-over; there is no dirty non-atomic data here for those to write back.
-// *last is 1 in the workgroup that must combine the slots.
-__device__ inline void publish_and_count(int* cnt, int nslices, int* last) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) *last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nslices - 1;
-    __syncthreads();
-}
-
 template <typename T, int MR, int NL, int THREADS> struct GemvShape {
     static constexpr int ES = sizeof(T);
     static constexpr int VEC = 16 / ES;
@@ -536,8 +512,8 @@ struct GemvWorkspace {
 static std::mutex g_ws_mu;
 static std::map<std::tuple<int, hipStream_t, int>, GemvWorkspace> g_ws;
 
-// kind 1: the split-K arrival counters (only gemv_kernel writes them, and every launch leaves them
-// at zero); kind 2: the strip partial slots.
+// kind 1: the GEMV's split-K arrival counters (every launch leaves them at zero); kind 2: its strip
+// partial slots; kinds 3 and 4: the same for the stream-K GEMM schedule (gemm_sk_workspace).
 static int get_workspace(hipStream_t stream, size_t need, void** out, int kind) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -583,6 +559,20 @@ static int split_buffers(hipStream_t stream, const GemvScratch* fixed, int64_t n
     rc = get_workspace(stream, part_bytes, &g.part, 2);
     if (rc) return rc;
     g.cnt = static_cast<int*>(cnt);
+    return 0;
+}
+
+// Buffers of the stream-K GEMM schedule (workspace kinds 3 and 4; the counters start at zero and
+// every launch leaves them at zero).
+int gemm_sk_workspace(hipStream_t stream, size_t cnt_ints, size_t slot_bytes, int** cnt, char** slots) {
+    void* c = nullptr;
+    void* p = nullptr;
+    int rc = get_workspace(stream, cnt_ints * sizeof(int), &c, 3);
+    if (rc) return rc;
+    rc = get_workspace(stream, slot_bytes, &p, 4);
+    if (rc) return rc;
+    *cnt = static_cast<int*>(c);
+    *slots = static_cast<char*>(p);
     return 0;
 }
 

@@ -94,6 +94,32 @@ __device__ inline float epilogue_value(float v, const GemmDesc& d, int64_t b, in
     return act_apply(v, d.act);
 }
 
+// Split-K hand-over between the workgroups that share one output block (a GEMV strip, a GEMM tile
+// split by the stream-K schedule).  Called by every thread after its partial-slot stores, which
+// carry the agent-scope cache policy (sc1: written through the XCD's L2 to the agent's coherence
+// point, never left dirty in an L2; the GEMV's agent-scope atomic stores compile to such stores, the
+// GEMM issues 16-byte buffer stores with the same bit).
+//  * Each wave waits until its own slot stores are acknowledged (s_waitcnt vmcnt(0); for a store
+//    the count drops when the write is complete at the scope it was issued with).  The asm's
+//    memory clobber keeps the compiler from moving the stores below the wait.
+//  * After the barrier every slot store of the workgroup is complete; thread 0 then counts the
+//    workgroup in with an agent-scope atomic add, so a count that completes the block is taken
+//    after every publisher's stores are complete.
+//  * The combining workgroup reads the slots with sc1 loads, which are served from the coherence
+//    point, issued after the count returned (through the barrier).
+// This is the ordering-only release that rocPRIM's look-back scan uses on this architecture for
+// data published through agent-scope atomics: a C++ release/acquire fence pair at agent scope
+// also writes back and invalidates the XCD's whole L2 (buffer_wbl2 sc1, buffer_inv sc1) once per
+// wave, which measured 104 us on c5 (x[1,4096] @ W[4096,11008] bf16) against 18.5 us with this
+// hand-over; there is no dirty non-atomic data here for those to write back.
+// *last is 1 in the workgroup that must combine the slots.
+__device__ inline void publish_and_count(int* cnt, int nslices, int* last) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) *last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nslices - 1;
+    __syncthreads();
+}
+
 // Operand load modes for one GEMM operand (A: rows m, B: rows n; "K-contiguous" means the
 // reduction index has stride 1).
 enum LoadMode : int {
@@ -103,7 +129,12 @@ enum LoadMode : int {
 };
 
 // Launchers (return hipError_t, or a negative TV_E_* code).
-int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream);
+// may_alloc = false: no launch path that needs a grown workspace (the stream-K schedule of the fp32
+// kernel); the plain data-parallel kernels serve the call.
+int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream, bool may_alloc = true);
+// Per-(device, stream) buffers of the stream-K GEMM schedule: `cnt_ints` arrival counters (zero
+// between launches) and `slot_bytes` of partial-accumulator slots.
+int gemm_sk_workspace(hipStream_t stream, size_t cnt_ints, size_t slot_bytes, int** cnt, char** slots);
 int launch_gemm_simt(const GemmDesc& d, hipStream_t stream);
 int launch_gemm_k0(const GemmDesc& d, hipStream_t stream); // K = 0: C = epilogue(0)
 int launch_repack(const tv_repack_args* a, hipStream_t stream);

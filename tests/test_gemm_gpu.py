@@ -5,11 +5,14 @@ Bars: int8 bit-exact (low byte of the exact sum, or the full int32 sum); fp32 wi
 fp32 accumulation allowance); integer-valued float inputs, whose sums every accumulation order
 reproduces exactly, bit-exact.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
 import oracle as orc
+import tensorvia_amd as tv
 from tensorvia_amd import rng
 from tests import golden
 from tests.util import (BFLOAT16, FLOAT16, FLOAT32, INT8, INT32, assert_fp32_close, assert_half_close,
@@ -130,6 +133,29 @@ def test_fp32_uniform_vs_oracle(hip, shape):
     b = rng.uniform_f32(9, K * N, -1, 1).reshape(K, N)
     c = to_storage(hip.gemm(to_torch(a, FLOAT32), to_torch(b, FLOAT32)))
     assert_fp32_close(c, orc.mul(a, FLOAT32, b, FLOAT32), orc.abs_bound(a, b), K)
+
+
+@pytest.mark.parametrize("batch,M,K,N", [(0, 2592, 2048, 4096), (0, 1300, 512, 4100), (2, 1000, 264, 2100),
+                                         (0, 1700, 1056, 2900)])
+def test_fp32_stream_k_bit_exact(hip, batch, M, K, N):
+    """fp32 tile counts that leave the last round of CUs partly idle (c1: 672 tiles, 2.625 per CU;
+    363, 272 and 322 tiles with ragged M/N tails, a batch, K of 9 and 33 k-tiles) run the stream-K
+    schedule, whose tiles are summed in segments by several workgroups.  Integer-valued inputs make
+    every order exact: bit-exact against exact sums, equal to the plain kernel (tv_hip_gemm_noalloc
+    takes no workspace, hence no stream-K), and equal on a second call."""
+    lead = (batch,) if batch else ()
+    a = ints(12, lead + (M, K), -3, 3)
+    b = ints(13, (K, N), -3, 3)
+    ta, tb = to_torch(a, FLOAT32), to_torch(b, FLOAT32)
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
+    c = to_storage(hip.gemm(ta, tb))
+    np.testing.assert_array_equal(c, want)
+    np.testing.assert_array_equal(to_storage(hip.gemm(ta, tb)), c)
+    plain = torch.zeros(lead + (M, N), dtype=torch.float32, device="cuda")
+    args = tv.make_args(ta, tb, plain)
+    tv.check(tv.lib().tv_hip_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(plain), c)
 
 
 def test_fp32_config1_full_size_sampled(hip):
