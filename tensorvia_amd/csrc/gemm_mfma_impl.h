@@ -697,9 +697,15 @@ __device__ inline void mfma_tile_of(int lin, int tiles_m, int tiles_n, int group
     tn = r / gsz;
 }
 
+// Waves per SIMD the kernels are compiled for: two, as the 8-wave tiles run.  For the 4-wave tiles
+// this is a register bound (at most 256 per wave) rather than an occupancy need: bound to one wave
+// per SIMD, the fp32 k-loop kept its accumulators in AGPRs and spent 28-32 v_accvgpr moves per
+// k-tile (324 instructions against 293); with the bound, 512 fp32 tiles ran 273 us against 311.
+template <class C> constexpr int mfma_waves_per_eu() { return C::THREADS == 256 ? 2 : C::THREADS / 256; }
+
 template <class C, bool FUSED = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
-                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
+                          amdgpu_waves_per_eu(mfma_waves_per_eu<C>(), mfma_waves_per_eu<C>())))
 void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec) {
     using Acc = typename Mfma<typename C::T>::Acc;
     constexpr int SMEM = 2 * C::STAGE > kEpiWaveBytes * C::THREADS / 64 ? 2 * C::STAGE : kEpiWaveBytes * C::THREADS / 64;
@@ -743,7 +749,7 @@ template <class C> constexpr int sk_slot_bytes() { return C::THREADS / 64 * C::F
 
 template <class C, bool FUSED = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
-                          amdgpu_waves_per_eu(2 * C::THREADS / 256, 2 * C::THREADS / 256))) // 2 per CU, as the plain kernel
+                          amdgpu_waves_per_eu(mfma_waves_per_eu<C>(), mfma_waves_per_eu<C>())))
 void gemm_mfma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec, SkArgs sk) {
     using Acc = typename Mfma<typename C::T>::Acc;
     static_assert(__is_same(Acc, f32x4), "stream-K slots hold fp32 accumulators");
@@ -851,16 +857,19 @@ static int sk_grid() {
     return cached[dev];
 }
 
-// The stream-K launch: K of at least 8 k-tiles, at least 8 k-tiles per workgroup.  Measured against
-// one workgroup per tile with random fp32 inputs (same box): c1 [2592,2048]@[2048,4096] 350-366
-// against 418-453 us; 512 / 768 / 1024 tiles of 128x128 (K 2048-4096) 11-13 % faster; [1024]^3
-// 37.1 against 70.9 us.  Returns 1 if it did not launch.
+// The stream-K launch: K of at least 32 k-tiles (8 when the tiles do not fill the CUs), at least 8
+// k-tiles per workgroup.  Measured against one workgroup per tile with random fp32 inputs (same
+// box, settled clocks): c1 [2592,2048]@[2048,4096] 349 against 380 us; 768 tiles 411 against
+// 432 us; 1024 tiles (K 1024-4096) 5-6 % faster; [1024]^3 (64 tiles) 37.9 against 68.0 us; but
+// 363 tiles at K = 512 (16 k-tiles) 78.7 against 75.0 us, the combines outweighing the balance.
+// Returns 1 if it did not launch.
 template <class C, bool FUSED>
 static int run_cfg_sk(const GemmDesc& d, hipStream_t stream, int group_m, int tiles_m, int tiles_n, int64_t ntiles, int c_vec) {
     const int nk = (d.K + C::BK - 1) / C::BK;
     if (nk < 8) return 1;
     int G = sk_grid<C>();
     if (G <= 0) return 1;
+    if (nk < 32 && ntiles >= G / 2) return 1; // G / 2: about one tile per CU
     const int64_t iters = ntiles * nk;
     if (iters / 8 < G) G = (int)(iters / 8);
     if (G < 1) return 1;

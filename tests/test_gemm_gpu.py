@@ -135,14 +135,14 @@ def test_fp32_uniform_vs_oracle(hip, shape):
     assert_fp32_close(c, orc.mul(a, FLOAT32, b, FLOAT32), orc.abs_bound(a, b), K)
 
 
-@pytest.mark.parametrize("batch,M,K,N", [(0, 2592, 2048, 4096), (0, 1300, 512, 4100), (2, 1000, 264, 2100),
-                                         (0, 1700, 1056, 2900)])
+@pytest.mark.parametrize("batch,M,K,N", [(0, 2592, 2048, 4096), (0, 1300, 1024, 4100), (2, 1000, 1056, 2100),
+                                         (0, 1700, 1056, 2900), (0, 300, 264, 500)])
 def test_fp32_stream_k_bit_exact(hip, batch, M, K, N):
-    """fp32 tile counts that leave the last round of CUs partly idle (c1: 672 tiles, 2.625 per CU;
-    363, 272 and 322 tiles with ragged M/N tails, a batch, K of 9 and 33 k-tiles) run the stream-K
-    schedule, whose tiles are summed in segments by several workgroups.  Integer-valued inputs make
-    every order exact: bit-exact against exact sums, equal to the plain kernel (tv_hip_gemm_noalloc
-    takes no workspace, hence no stream-K), and equal on a second call."""
+    """fp32 GEMMs on the stream-K schedule, whose tiles are summed in segments by several
+    workgroups: c1 (672 tiles, 2.625 per CU); 363, 272 and 322 tiles with ragged M/N tails and a
+    batch (K of 32 and 33 k-tiles); 12 tiles at K = 9 k-tiles (fewer tiles than CUs).  Integer-valued
+    inputs make every order exact: bit-exact against exact sums, equal to the plain kernel
+    (tv_hip_gemm_noalloc takes no workspace, hence no stream-K), and equal on a second call."""
     lead = (batch,) if batch else ()
     a = ints(12, lead + (M, K), -3, 3)
     b = ints(13, (K, N), -3, 3)
