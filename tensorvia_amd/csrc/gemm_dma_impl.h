@@ -318,10 +318,18 @@ __device__ inline void write_tile_wg_i8(const i32x4 (&acc)[C::FM][C::FN], char* 
     }
 }
 
-template <class C, bool FUSED = false>
-__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
-                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
-void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec) {
+// LDS of the direct-load kernels: [A stage 0 | A stage 1 | B stage 0 | B stage 1]; the epilogue
+// reuses all of it.
+template <class C> constexpr int dma_lds_bytes() {
+    return 2 * (DmaOperand<C::AMODE, C::BM, C::THREADS, C::ES>::BYTES + DmaOperand<C::BMODE, C::BN, C::THREADS, C::ES>::BYTES);
+}
+
+// The k-loop of one output tile over k-tiles [kt0, kt1) into acc (zeroed by the caller).  L: the
+// kernel's LDS (dma_lds_bytes).  The loaders see K as the range's end, so every load past it
+// returns zeros.
+template <class C>
+__device__ __attribute__((always_inline)) inline void dma_tile_kloop(const GemmDesc& d, char* L, int b, int m0, int n0, int kt0,
+                                                                     int kt1, typename Mfma<typename C::T>::Acc (&acc)[C::FM][C::FN]) {
     using T = typename C::T;
     using Op = Mfma<T>;
     using Acc = typename Op::Acc;
@@ -332,54 +340,30 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
     constexpr int NWAVES = C::THREADS / 64;
     static_assert(NWAVES % 2 == 0, "the epilogue gives half of the waves to each stage array");
     constexpr int EPI = STAGE / (NWAVES / 2) / 16 * 16; // staging bytes per wave in the epilogue
-
-    // LDS: [A stage 0 | A stage 1 | B stage 0 | B stage 1]; the epilogue reuses all of it.
-    __shared__ __attribute__((aligned(1024))) char L[2 * STAGE];
     char* const S0 = L;
     char* const S1 = L + STAGE;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+    (void)S0; (void)S1; (void)EPI; (void)tid;
     const unsigned LA0 = (unsigned)(uintptr_t)(lds_void*)L;
     const unsigned LB0 = LA0 + 2 * LA::BYTES;
     static_assert(LA::BYTES + 16384 + 2048 < 65536 && LB::BYTES + 16384 + 2048 < 65536 &&
                       LA::BYTES + (C::FM - 1) * 2048 < 65536 && LB::BYTES + (C::FN - 1) * 2048 < 65536,
                   "stage 1 and fragment offsets must fit a ds_read immediate");
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
-
-    // Workgroup -> tile (XCD-aware, groups of group_m tile-rows), as gemm_mfma_kernel.
-    int bid = blockIdx.x;
-    const int nwg = gridDim.x;
-    if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
-    const int per_batch = tiles_m * tiles_n;
-    const int b = bid / per_batch;
-    int r = bid - b * per_batch;
-    const int span = group_m * tiles_n;
-    const int g = r / span;
-    const int first_m = g * group_m;
-    const int gsz = min(tiles_m - first_m, group_m);
-    r -= g * span;
-    const int tm = first_m + r % gsz;
-    const int tn = r / gsz;
-    const int m0 = tm * C::BM, n0 = tn * C::BN;
+    const int K_eff = min(d.K, kt1 * C::BK);
 
     LA la;
     la.base = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + (int64_t)m0 * d.sa_m) * ES;
-    la.s_r = d.sa_m; la.s_k = d.sa_k; la.rows_valid = d.M - m0; la.K = d.K;
+    la.s_r = d.sa_m; la.s_k = d.sa_k; la.rows_valid = d.M - m0; la.K = K_eff;
     LB lb;
     lb.base = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)n0 * d.sb_n) * ES;
-    lb.s_r = d.sb_n; lb.s_k = d.sb_k; lb.rows_valid = d.N - n0; lb.K = d.K;
+    lb.s_r = d.sb_n; lb.s_k = d.sb_k; lb.rows_valid = d.N - n0; lb.K = K_eff;
     la.init(wave, lane);
     lb.init(wave, lane);
     la.xinit(LA0, lane, wm * C::WM);
     lb.xinit(LB0, lane, wn * C::WN);
-
-    Acc acc[C::FM][C::FN];
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
 
     // A fragments: one set, each reloaded with the next k-group's right after its row of MFMAs.
     // B fragments: one set per k-group of the k-tile (every row of a k-group uses all of them).
@@ -444,12 +428,11 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
         wait_lgkmcnt<C::FM - C::FN + 1>();
     };
 
-    const int nk = (d.K + C::BK - 1) / C::BK;
-    // Prologue: tiles 0 and 1 in flight, then k-group 0 of tile 0.
-    la.issue(S0, wave, 0);
-    lb.issue(L + 2 * LA::BYTES, wave, 0);
-    la.issue(L + LA::BYTES, wave, C::BK); // all out of range (zeros) when nk == 1
-    lb.issue(L + 2 * LA::BYTES + LB::BYTES, wave, C::BK);
+    // Prologue: k-tiles kt0 and kt0 + 1 in flight, then k-group 0 of kt0.
+    la.issue(L, wave, kt0 * C::BK);
+    lb.issue(L + 2 * LA::BYTES, wave, kt0 * C::BK);
+    la.issue(L + LA::BYTES, wave, (kt0 + 1) * C::BK); // all out of range (zeros) past the range
+    lb.issue(L + 2 * LA::BYTES + LB::BYTES, wave, (kt0 + 1) * C::BK);
     wait_vmcnt<NDMA>();
     lds_barrier();
 #pragma unroll
@@ -458,17 +441,42 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
     for (int i = 0; i < C::FM; ++i) fa[i] = la.frag_at(0, 0, i);
     wait_lgkmcnt<C::FM - 1>();
 
-    // The step count is rounded up to even: a step past K multiplies the zeros loaded there, and
-    // the loop has no conditional tail (the accumulators stay in place across the loop).
-    for (int kt = 0; kt < nk; kt += 2) {
+    // The step count is rounded up to even: a step past the range multiplies the zeros loaded there
+    // (the loaders' K is the range's end), and the loop has no conditional tail (the accumulators
+    // stay in place across the loop).
+    for (int kt = kt0; kt < kt1; kt += 2) {
         step(0, kt);
         step(1, kt + 1);
     }
-
-    // Epilogue.  The zero-filling loads issued by the last steps land before anything else (no
-    // load into LDS is left in flight when the workgroup ends); all waves leave the k-loop's LDS
-    // before any wave stages its output there.
+    // The zero-filling loads issued by the last steps land before anything else (no load into LDS
+    // is left in flight when the range ends).
     wait_vmcnt<0>();
+
+}
+
+// Store of one output tile (the epilogue).  acc[i][j][q] is tile row wm*WM + 16i + lane%16,
+// column wn*WN + 16j + 4*(lane/16) + q.
+template <class C, bool FUSED>
+__device__ __attribute__((always_inline)) inline void dma_tile_store(const GemmDesc& d, char* L, int b, int m0, int n0, int c_vec,
+                                                                     const typename Mfma<typename C::T>::Acc (&acc)[C::FM][C::FN]) {
+    using T = typename C::T;
+    using Op = Mfma<T>;
+    using Acc = typename Op::Acc;
+    constexpr int ES = C::ES;
+    using LA = DmaOperand<C::AMODE, C::BM, C::THREADS, ES>;
+    using LB = DmaOperand<C::BMODE, C::BN, C::THREADS, ES>;
+    constexpr int STAGE = LA::BYTES + LB::BYTES;
+    constexpr int NWAVES = C::THREADS / 64;
+    static_assert(NWAVES % 2 == 0, "the epilogue gives half of the waves to each stage array");
+    constexpr int EPI = STAGE / (NWAVES / 2) / 16 * 16; // staging bytes per wave in the epilogue
+    char* const S0 = L;
+    char* const S1 = L + STAGE;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+    (void)S0; (void)S1; (void)EPI; (void)tid;
+    // All waves leave the k-loop's LDS before any wave stages its output there (the barriers below).
     const size_t csz = dtype_size(d.dtype_c);
     char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
     if constexpr (FUSED && !__is_same(Acc, i32x4)) {
@@ -517,6 +525,99 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
         if (d.dtype_c == TV_BFLOAT16) write_tile<__bf16, C>(acc, Cb, row0, col0, vec_ok, d);
         else if (d.dtype_c == TV_FLOAT16) write_tile<_Float16, C>(acc, Cb, row0, col0, vec_ok, d);
         else write_tile<float, C>(acc, Cb, row0, col0, vec_ok, d);
+    }
+}
+
+template <class C, bool FUSED = false>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
+                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
+void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec) {
+    using Acc = typename Mfma<typename C::T>::Acc;
+    __shared__ __attribute__((aligned(1024))) char L[dma_lds_bytes<C>()];
+    // Workgroup -> tile (XCD-aware, groups of group_m tile-rows), as gemm_mfma_kernel.
+    int bid = blockIdx.x;
+    const int nwg = gridDim.x;
+    if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+    int b, tm, tn;
+    mfma_tile_of(bid, tiles_m, tiles_n, group_m, b, tm, tn);
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
+    Acc acc[C::FM][C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+    dma_tile_kloop<C>(d, L, b, m0, n0, 0, (d.K + C::BK - 1) / C::BK, acc);
+    dma_tile_store<C, FUSED>(d, L, b, m0, n0, c_vec, acc);
+}
+
+// Stream-K schedule of the direct-load kernel, as gemm_mfma_sk_kernel (same iteration ranges, slots
+// and hand-over; int32 accumulators of int8 sum exactly in any order).
+template <class C, bool FUSED = false>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
+                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
+void gemm_dma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec, SkArgs sk) {
+    using Acc = typename Mfma<typename C::T>::Acc;
+    constexpr int SLOT = sk_slot_bytes<C>();
+    __shared__ __attribute__((aligned(1024))) char L[dma_lds_bytes<C>()];
+    __shared__ int last_flag;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = gridDim.x;
+    int w = blockIdx.x;
+    if ((G & 7) == 0) w = (w & 7) * (G >> 3) + (w >> 3);
+    const int64_t I = sk.iters;
+    const int nk = sk.nk;
+    const int64_t it_end = (int64_t)(w + 1) * I / G;
+    auto owner = [&](int64_t it) { return (int)(((it + 1) * G - 1) / I); };
+    auto slot_rsrc = [&](int slot) { return make_rsrc(sk.slots + (int64_t)slot * SLOT, SLOT); };
+
+    for (int64_t it = (int64_t)w * I / G; it < it_end;) {
+        const int tile = (int)(it / nk);
+        const int kt0 = (int)(it - (int64_t)tile * nk);
+        const int kt1 = (int)min((int64_t)nk, kt0 + (it_end - it));
+        it += kt1 - kt0;
+        int b, tm, tn;
+        mfma_tile_of(tile, tiles_m, tiles_n, group_m, b, tm, tn);
+        const int m0 = tm * C::BM, n0 = tn * C::BN;
+        Acc acc[C::FM][C::FN];
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+        lds_barrier(); // the previous segment's epilogue is done with the LDS
+        dma_tile_kloop<C>(d, L, b, m0, n0, kt0, kt1, acc);
+        if (kt0 != 0 || kt1 != nk) {
+            const int64_t t0 = (int64_t)tile * nk;
+            const int first = owner(t0), last = owner(t0 + nk - 1);
+            {
+                const __amdgpu_buffer_rsrc_t r = slot_rsrc(w == first ? 2 * w + 1 : 2 * w);
+#pragma unroll
+                for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < C::FN; ++j)
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[i][j]), r,
+                                                               (((wave * C::FM + i) * C::FN + j) * 64 + lane) * 16, 0, 16);
+            }
+            publish_and_count(sk.cnt + tile, last - first + 1, &last_flag);
+            if (!last_flag) continue;
+            for (int v = first; v <= last; ++v) {
+                const __amdgpu_buffer_rsrc_t r = slot_rsrc(v == first ? 2 * v + 1 : 2 * v);
+#pragma unroll
+                for (int i = 0; i < C::FM; ++i) {
+#pragma unroll
+                    for (int j = 0; j < C::FN; ++j) {
+                        const Acc p = __builtin_bit_cast(
+                            Acc, __builtin_amdgcn_raw_buffer_load_b128(r, (((wave * C::FM + i) * C::FN + j) * 64 + lane) * 16, 0, 16));
+                        acc[i][j] = v == first ? p : acc[i][j] + p;
+                    }
+                    // one row of slot loads at a time: with all of them hoisted, the loads and the
+                    // 128 accumulator registers exceed the 256 a wave has
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            if (threadIdx.x == 0) __hip_atomic_store(sk.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        dma_tile_store<C, FUSED>(d, L, b, m0, n0, c_vec, acc);
     }
 }
 
@@ -696,8 +797,47 @@ void gemm_smallk_kernel(GemmDesc d, int tiles_m, int tiles_n) {
     wait_vmcnt<0>();
 }
 
+// Stream-K launch of the direct-load kernel (one resident workgroup per CU: 128 KB of LDS) for few,
+// long tiles: at most a quarter as many 256x256 tiles as resident workgroups and K of at least 64
+// k-tiles.  A split 256x256 tile moves 256 KB per segment through the slots, which costs more than
+// the balance gains once the tiles are many.  Measured (settled clocks, same box, against one
+// workgroup per tile): bf16 [512,8192]@[8192,8192] 88.9 against 146.7 us, [128,8192]@[8192,8192]
+// 80.6 against 145 us, [1024,4096]@[4096,4096] 62.0 against 77.3 us; int8 [512,8192]@[8192,8192]
+// 52.0 against 75.5 us; but 192 tiles (M = 3000, K = 4096) 121.5 against 83.0 us in bf16, and 128
+// tiles slower too.  c2 (256 tiles) and c3 (2048) keep one workgroup per tile.  Returns 1 if it did
+// not launch.
+template <class C, bool FUSED>
+static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int tiles_m, int tiles_n, int64_t ntiles, int c_vec) {
+    const int nk = (d.K + C::BK - 1) / C::BK;
+    if (nk < 64) return 1;
+    static int grid[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+    if (grid[dev] <= 0) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(gemm_dma_sk_kernel<C, false>), C::THREADS,
+                                                         0) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
+            return 1;
+        grid[dev] = per_cu * cus;
+    }
+    int G = grid[dev];
+    if (ntiles * 4 > G) return 1;
+    const int64_t iters = ntiles * nk;
+    if (iters / 8 < G) G = (int)(iters / 8);
+    if (G < 1) return 1;
+    SkArgs sk;
+    sk.iters = iters;
+    sk.nk = nk;
+    const int rc = gemm_sk_workspace(stream, (size_t)ntiles, (size_t)2 * G * sk_slot_bytes<C>(), &sk.cnt, &sk.slots);
+    if (rc) return rc;
+    hipLaunchKernelGGL((gemm_dma_sk_kernel<C, FUSED>), dim3((unsigned)G), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n, group_m,
+                       c_vec, sk);
+    return hipGetLastError();
+}
+
 template <class C>
-static int run_dma_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
+static int run_dma_cfg(const GemmDesc& d, hipStream_t stream, int group_m, bool may_alloc) {
     const int tiles_m = (d.M + C::BM - 1) / C::BM;
     const int tiles_n = (d.N + C::BN - 1) / C::BN;
     const int64_t nwg = (int64_t)tiles_m * tiles_n * d.batch;
@@ -713,6 +853,15 @@ static int run_dma_cfg(const GemmDesc& d, hipStream_t stream, int group_m) {
     // The fused epilogue runs in the staged store only (16-byte aligned rows of C).
     const bool epi = d.bias != nullptr || d.act != TV_ACT_NONE;
     if (epi && d.sc_n != 1) return TV_E_UNSUPPORTED; // the fused store writes rows of C
+    if (may_alloc) {
+        int rc = 1;
+        if constexpr (!__is_same(typename C::T, int8_t))
+            rc = epi ? run_dma_sk<C, true>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec)
+                     : run_dma_sk<C, false>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec);
+        else
+            rc = run_dma_sk<C, false>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec);
+        if (rc != 1) return rc;
+    }
     if constexpr (!__is_same(typename C::T, int8_t))
         if (epi) {
             hipLaunchKernelGGL((gemm_dma_kernel<C, true>), dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
@@ -754,7 +903,7 @@ static bool smallk_ok(const GemmDesc& d, int es, int bm_rows, int bn_rows) {
 
 // 16-bit / int8 inputs: direct-to-LDS kernel for the vector layouts, gemm_mfma_kernel otherwise.
 template <typename T, int BM, int BN, int WMW, int WNW>
-static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m) {
+static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m, bool may_alloc) {
     const int es = (int)sizeof(T);
     const int am = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, BM);
     const int bm = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, BN);
@@ -770,13 +919,13 @@ static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m) {
 #undef TV_CASE
     }
 #define TV_CASE(A_, B_) \
-    if (am == A_ && bm == B_) return run_dma_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream, group_m);
+    if (am == A_ && bm == B_) return run_dma_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream, group_m, may_alloc);
     TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)
     TV_CASE(LOAD_KCONTIG, LOAD_KCONTIG)
     TV_CASE(LOAD_MNCONTIG, LOAD_MNCONTIG)
     TV_CASE(LOAD_MNCONTIG, LOAD_KCONTIG)
 #undef TV_CASE
-    return run_modes<T, BM, BN, WMW, WNW>(d, stream, group_m);
+    return run_modes<T, BM, BN, WMW, WNW>(d, stream, group_m, may_alloc);
 }
 
 } // namespace tvk

@@ -2,7 +2,7 @@
 #include "gemm_dma_impl.h"
 
 namespace tvk {
-int launch_gemm_mfma_i8(const GemmDesc& d, hipStream_t stream) {
-    return run_modes_dma<int8_t, 256, 256, 2, 4>(d, stream, 8);
+int launch_gemm_mfma_i8(const GemmDesc& d, hipStream_t stream, bool may_alloc) {
+    return run_modes_dma<int8_t, 256, 256, 2, 4>(d, stream, 8, may_alloc);
 }
 } // namespace tvk

@@ -125,6 +125,15 @@ def test_direct_load_column_bias_vector_rows(dt_in, dt_out, act, bias_kind):
     run_case(dt_in, dt_out, 2, 300, 256, 264, bias_kind, act, seed=21, pad=16)
 
 
+@pytest.mark.parametrize("act", [tv.ACT_SILU, tv.ACT_TANH])
+@pytest.mark.parametrize("bias_kind", ["col", "full"])
+def test_stream_k_fused(act, bias_kind):
+    """The fused epilogue on the stream-K schedules: bf16 with 6 tiles of 256x256 (direct-load
+    kernel) and fp32 with 12 tiles of 128x128, both over K long enough to split every tile."""
+    run_case(tv.BFLOAT16, tv.BFLOAT16, 0, 300, 4096, 700, bias_kind, act, seed=31)
+    run_case(tv.FLOAT32, tv.FLOAT32, 0, 300, 2048, 500, bias_kind, act, seed=32)
+
+
 @pytest.mark.parametrize("act", [tv.ACT_RELU, tv.ACT_SILU])
 def test_bf16_in_fp32_out(act):
     run_case(tv.BFLOAT16, tv.FLOAT32, 0, 260, 320, 300, "col", act, seed=2)

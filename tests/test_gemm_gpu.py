@@ -263,6 +263,39 @@ def test_small_k_persistent_exact(hip, dt, K, bt):
     np.testing.assert_array_equal(c, want)
 
 
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, INT8])
+@pytest.mark.parametrize("batch,M,K,N", [(0, 512, 8192, 1024), (0, 300, 8192, 700), (2, 200, 8192, 520), (0, 1000, 8208, 1000)])
+def test_direct_load_stream_k_bit_exact(hip, dt, batch, M, K, N):
+    """16-bit and int8 GEMMs with few, long 256x256 tiles (8, 6, 6 and 16 tiles; K = 8192 and a
+    ragged 8208) run the direct-load kernel's stream-K schedule: tiles summed in segments by
+    several workgroups.  Integer-valued inputs: exact fp32 / int32 sums in any order, so the half
+    outputs are the exact sums rounded once, int8 the low byte, and everything equals the plain
+    kernel's result (tv_hip_gemm_noalloc takes no workspace, hence no stream-K)."""
+    lead = (batch,) if batch else ()
+    if dt == INT8:
+        x = ints(14, lead + (M, K), -128, 127, np.int8)
+        y = ints(15, (K, N), -128, 127, np.int8)
+        xs, ys = x, y
+    else:
+        x = ints(14, lead + (M, K), -3, 3)
+        y = ints(15, (K, N), -3, 3)
+        xs, ys = half_bits(x, dt), half_bits(y, dt)
+    ta, tb = to_torch(xs, dt), to_torch(ys, dt)
+    exact = np.matmul(x.astype(np.float64), y.astype(np.float64))
+    c = to_storage(hip.gemm(ta, tb))
+    if dt == INT8:
+        np.testing.assert_array_equal(c, orc.low_byte(exact.astype(np.int64)))
+        c32 = to_storage(hip.gemm(ta, tb, out_dtype=INT32))
+        np.testing.assert_array_equal(c32, exact.astype(np.int32))
+    else:
+        np.testing.assert_array_equal(c, half_bits(exact.astype(np.float32), dt))
+    plain = torch.zeros(lead + (M, N), dtype=ta.dtype, device="cuda")
+    args = tv.make_args(ta, tb, plain)
+    tv.check(tv.lib().tv_hip_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(plain), c)
+
+
 # ---- views, offsets, batches ----------------------------------------------------------------
 
 @pytest.mark.parametrize("dt", [FLOAT32, BFLOAT16, INT8])
