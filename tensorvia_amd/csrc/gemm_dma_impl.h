@@ -324,29 +324,83 @@ template <class C> constexpr int dma_lds_bytes() {
     return 2 * (DmaOperand<C::AMODE, C::BM, C::THREADS, C::ES>::BYTES + DmaOperand<C::BMODE, C::BN, C::THREADS, C::ES>::BYTES);
 }
 
+// One k-tile of the direct-load pipeline for one wave.  Stage `cs` holds k-tile t, whose k-group 0
+// is already in fa / fb0; stage 1 - cs holds k-tile t + 1 once the barrier has passed.
+//   Region 1: rows on k-group 0; after row i reload fa[i] with k-group 1 and read fb1[i].
+//   Wait until at most VMW vector-memory operations of this wave are in flight, i.e. tile t + 1's
+//   loads have landed when exactly VMW operations were issued after them (0 here; stores issued
+//   after them for a caller that passes their count), barrier (tile t + 1 visible, stage cs
+//   free).
+//   Region 2: rows on k-group 1; one load of the k-tile at k offset k2 into stage cs per row;
+//   after row i reload fa[i] with k-group 0 of tile t + 1 and read its fb0[i].
+template <class C, int VMW, class LA, class LB, class Acc>
+__device__ __attribute__((always_inline)) inline void dma_kstep(int cs, int k2, const LA& la, const LB& lb, u32x4 (&fa)[C::FM],
+                                                                u32x4 (&fb0)[C::FN], u32x4 (&fb1)[C::FN], Acc (&acc)[C::FM][C::FN],
+                                                                unsigned LA0, unsigned LB0, int wave) {
+    using Op = Mfma<typename C::T>;
+    constexpr int NA = LA::PER_WAVE, NB = LB::PER_WAVE, NDMA = NA + NB;
+    static_assert(NDMA <= C::FM, "one load per row of MFMAs");
+    // Reads after each row: the row's A reload, plus B fragment i after rows i < FN.
+    static_assert(C::FN <= C::FM, "one B fragment per row");
+    constexpr int RD_B = 1 + LB::kFragReads;
+    auto row = [&](int i, const u32x4 (&fb)[C::FN]) {
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) Op::run(fb[j], fa[i], acc[i][j]); // B fragment first: lanes hold 4 columns
+    };
+    // Interleave of a region: each row's FN MFMAs, then the reads that follow that row.
+    auto sched_rows = [] {
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, C::FN, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, RD_B, 0);
+        }
+#pragma unroll
+        for (int i = C::FN; i < C::FM; ++i) {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, C::FN, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const int ns = 1 - cs;
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) {
+        row(i, fb0);
+        fa[i] = la.frag_at(cs, 1, i);
+        if (i < C::FN) fb1[i] = lb.frag_at(cs, 1, i);
+    }
+    sched_rows();
+    const __amdgpu_buffer_rsrc_t ra = la.rsrc(k2);
+    const __amdgpu_buffer_rsrc_t rb = lb.rsrc(k2);
+    wait_vmcnt<VMW>();
+    dma_barrier();
+    const unsigned sa = LA0 + (unsigned)(cs * LA::BYTES), sb = LB0 + (unsigned)(cs * LB::BYTES);
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) {
+        row(i, fb1);
+        if (i < NA) la.issue_one(i, ra, sa, wave, k2);
+        else if (i < NDMA) lb.issue_one(i - NA, rb, sb, wave, k2);
+        if (i < C::FN) fb0[i] = lb.frag_at(ns, 0, i);
+        fa[i] = la.frag_at(ns, 0, i);
+    }
+    sched_rows();
+    // Row 0 of the next step needs fb0 and fa[0]: only the A reloads after the last B read
+    // may still be in flight.
+    wait_lgkmcnt<C::FM - C::FN + 1>();
+}
+
 // The k-loop of one output tile over k-tiles [kt0, kt1) into acc (zeroed by the caller).  L: the
 // kernel's LDS (dma_lds_bytes).  The loaders see K as the range's end, so every load past it
 // returns zeros.
 template <class C>
 __device__ __attribute__((always_inline)) inline void dma_tile_kloop(const GemmDesc& d, char* L, int b, int m0, int n0, int kt0,
                                                                      int kt1, typename Mfma<typename C::T>::Acc (&acc)[C::FM][C::FN]) {
-    using T = typename C::T;
-    using Op = Mfma<T>;
-    using Acc = typename Op::Acc;
     constexpr int ES = C::ES;
     using LA = DmaOperand<C::AMODE, C::BM, C::THREADS, ES>;
     using LB = DmaOperand<C::BMODE, C::BN, C::THREADS, ES>;
-    constexpr int STAGE = LA::BYTES + LB::BYTES;
-    constexpr int NWAVES = C::THREADS / 64;
-    static_assert(NWAVES % 2 == 0, "the epilogue gives half of the waves to each stage array");
-    constexpr int EPI = STAGE / (NWAVES / 2) / 16 * 16; // staging bytes per wave in the epilogue
-    char* const S0 = L;
-    char* const S1 = L + STAGE;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
-    (void)S0; (void)S1; (void)EPI; (void)tid;
     const unsigned LA0 = (unsigned)(uintptr_t)(lds_void*)L;
     const unsigned LB0 = LA0 + 2 * LA::BYTES;
     static_assert(LA::BYTES + 16384 + 2048 < 65536 && LB::BYTES + 16384 + 2048 < 65536 &&
@@ -368,64 +422,9 @@ __device__ __attribute__((always_inline)) inline void dma_tile_kloop(const GemmD
     // A fragments: one set, each reloaded with the next k-group's right after its row of MFMAs.
     // B fragments: one set per k-group of the k-tile (every row of a k-group uses all of them).
     u32x4 fa[C::FM], fb0[C::FN], fb1[C::FN];
-    auto row = [&](int i, const u32x4 (&fb)[C::FN]) {
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j) Op::run(fb[j], fa[i], acc[i][j]); // B fragment first: lanes hold 4 columns
-    };
-    constexpr int NA = LA::PER_WAVE, NB = LB::PER_WAVE, NDMA = NA + NB;
-    static_assert(NDMA <= C::FM, "one load per row of MFMAs");
-    // Reads after each row: the row's A reload, plus B fragment i after rows i < FN.
-    static_assert(C::FN <= C::FM, "one B fragment per row");
-    constexpr int RD_B = 1 + LB::kFragReads;
-
-    // Interleave of a region: each row's FN MFMAs, then the reads that follow that row.
-    auto sched_rows = [] {
-#pragma unroll
-        for (int i = 0; i < C::FN; ++i) {
-            __builtin_amdgcn_sched_group_barrier(SG_MFMA, C::FN, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, RD_B, 0);
-        }
-#pragma unroll
-        for (int i = C::FN; i < C::FM; ++i) {
-            __builtin_amdgcn_sched_group_barrier(SG_MFMA, C::FN, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    };
-
-    // One k-tile: stage `cs` holds tile kt (k-group 0 already in fa / fb0); stage 1 - cs holds
-    // tile kt + 1 once the barrier has passed.
-    //   Region 1: rows on k-group 0; after row i reload fa[i] with k-group 1 and read fb1[i].
-    //   Wait for tile kt+1's loads, barrier (tile kt+1 visible, stage cs free).
-    //   Region 2: rows on k-group 1; one load of tile kt+2 into stage cs per row; after row i
-    //   reload fa[i] with k-group 0 of tile kt+1 and read its fb0[i].
+    constexpr int NDMA = LA::PER_WAVE + LB::PER_WAVE;
     auto step = [&](int cs, int kt) {
-        const int ns = 1 - cs;
-#pragma unroll
-        for (int i = 0; i < C::FM; ++i) {
-            row(i, fb0);
-            fa[i] = la.frag_at(cs, 1, i);
-            if (i < C::FN) fb1[i] = lb.frag_at(cs, 1, i);
-        }
-        sched_rows();
-        const int k2 = (kt + 2) * C::BK;
-        const __amdgpu_buffer_rsrc_t ra = la.rsrc(k2);
-        const __amdgpu_buffer_rsrc_t rb = lb.rsrc(k2);
-        wait_vmcnt<0>();
-        dma_barrier();
-        const unsigned sa = LA0 + (unsigned)(cs * LA::BYTES), sb = LB0 + (unsigned)(cs * LB::BYTES);
-#pragma unroll
-        for (int i = 0; i < C::FM; ++i) {
-            row(i, fb1);
-            if (i < NA) la.issue_one(i, ra, sa, wave, k2);
-            else if (i < NDMA) lb.issue_one(i - NA, rb, sb, wave, k2);
-            if (i < C::FN) fb0[i] = lb.frag_at(ns, 0, i);
-            fa[i] = la.frag_at(ns, 0, i);
-        }
-        sched_rows();
-        // Row 0 of the next step needs fb0 and fa[0]: only the A reloads after the last B read
-        // may still be in flight.
-        wait_lgkmcnt<C::FM - C::FN + 1>();
+        dma_kstep<C, 0>(cs, (kt + 2) * C::BK, la, lb, fa, fb0, fb1, acc, LA0, LB0, wave);
     };
 
     // Prologue: k-tiles kt0 and kt0 + 1 in flight, then k-group 0 of kt0.
@@ -451,7 +450,6 @@ __device__ __attribute__((always_inline)) inline void dma_tile_kloop(const GemmD
     // The zero-filling loads issued by the last steps land before anything else (no load into LDS
     // is left in flight when the range ends).
     wait_vmcnt<0>();
-
 }
 
 // Store of one output tile (the epilogue).  acc[i][j][q] is tile row wm*WM + 16i + lane%16,
@@ -797,6 +795,157 @@ void gemm_smallk_kernel(GemmDesc d, int tiles_m, int tiles_n) {
     wait_vmcnt<0>();
 }
 
+// Persistent direct-load GEMM for launches of several tiles per CU (one resident workgroup per
+// CU).  The k-loop runs on from one tile into the next: the last two k-steps of a tile load
+// k-tiles 0 and 1 of the workgroup's next tile, so when a tile's output is stored the next tile's
+// first k-tile has landed, its k-group-0 fragments are in registers, and its second k-tile is
+// loading.  One workgroup per tile instead loads its first two k-tiles only after the previous
+// workgroup on the CU has stored its output.
+//  * The output is staged through an LDS area of its own (the k-loop's stages hold the next
+//    tile's operands), 16 rows per pass and wave.  The next tile's first step waits for the
+//    stores along with its k-tile 1 loads (vmcnt retires in issue order), after a region of
+//    MFMAs.
+//  * Workgroup s of XCD x (ids x, x + 8, ...) takes the tiles lo + s, lo + s + S, ... of its XCD's
+//    range [lo, hi) (S: the XCD's workgroups), the order in which one workgroup per tile would run
+//    them, so the tiles in flight on an XCD share A and B rows in its L2 as before.
+//  * 16-bit inputs and outputs, with 16-byte aligned rows (an fp32 staging area does not fit
+//    beside the stages; int8 outputs keep the one-per-tile kernel, whose store writes whole
+//    256-byte rows of the tile: 1 % faster there than this kernel's 64-byte wave rows).
+//  * Same bits as one workgroup per tile (the same k-loop per tile).  Measured on one box against
+//    it: c3 829 against 830 us, [8192]^3 788 against 806, [4096,1024] @ [1024,32768] 241 against
+//    260 (the fixed cost per tile saved is a larger share at short K).
+template <class C>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
+                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
+void gemm_dma_chain_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int ntiles) {
+    using T = typename C::T;
+    using Acc = typename Mfma<T>::Acc;
+    static_assert(!__is_same(T, int8_t), "16-bit inputs");
+    constexpr int ES = C::ES;
+    using LA = DmaOperand<C::AMODE, C::BM, C::THREADS, ES>;
+    using LB = DmaOperand<C::BMODE, C::BN, C::THREADS, ES>;
+    constexpr int NWAVES = C::THREADS / 64;
+    constexpr int EPI = kSmallKEpiBytes; // 16 rows of a 64-column 16-bit row, padded
+    constexpr int NDMA = LA::PER_WAVE + LB::PER_WAVE;
+    __shared__ __attribute__((aligned(1024))) char L[dma_lds_bytes<C>()];
+    __shared__ __attribute__((aligned(16))) char E[EPI * NWAVES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+    const unsigned LA0 = (unsigned)(uintptr_t)(lds_void*)L;
+    const unsigned LB0 = LA0 + 2 * LA::BYTES;
+
+    int s = blockIdx.x, S = gridDim.x, lo = 0, hi = ntiles;
+    if ((gridDim.x & 7) == 0) {
+        const int x = blockIdx.x & 7;
+        s = blockIdx.x >> 3;
+        S = gridDim.x >> 3;
+        lo = (int)((int64_t)x * ntiles / 8);
+        hi = (int)((int64_t)(x + 1) * ntiles / 8);
+    }
+    int t = lo + s;
+    if (t >= hi) return;
+
+    LA la;
+    LB lb;
+    la.s_r = d.sa_m; la.s_k = d.sa_k; la.K = d.K;
+    lb.s_r = d.sb_n; lb.s_k = d.sb_k; lb.K = d.K;
+    la.xinit(LA0, lane, wm * C::WM);
+    lb.xinit(LB0, lane, wn * C::WN);
+    // Points the loaders at tile u; past the range every lane is out of range and loads zeros.
+    // Lane-derived values of the loaders' and the store's addressing are computed where they are
+    // used, from a copy of the lane id that the compiler cannot hoist: kept live across the k-loop
+    // they would not fit the 256 registers of a wave.
+    auto lane_here = [&] {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        return ln;
+    };
+    auto point = [&](int u) {
+        const int ln = lane_here();
+        const bool live = u < hi;
+        int b, tm, tn;
+        mfma_tile_of(live ? u : t, tiles_m, tiles_n, group_m, b, tm, tn);
+        const int m0 = tm * C::BM, n0 = tn * C::BN;
+        la.base = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + (int64_t)m0 * d.sa_m) * ES;
+        la.rows_valid = live ? d.M - m0 : 0;
+        lb.base = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)n0 * d.sb_n) * ES;
+        lb.rows_valid = live ? d.N - n0 : 0;
+        la.init(wave, ln);
+        lb.init(wave, ln);
+    };
+
+    u32x4 fa[C::FM], fb0[C::FN], fb1[C::FN];
+    // Prologue: k-tiles 0 and 1 of the first tile.
+    point(t);
+    la.issue(L, wave, 0);
+    lb.issue(L + 2 * LA::BYTES, wave, 0);
+    la.issue(L + LA::BYTES, wave, C::BK);
+    lb.issue(L + 2 * LA::BYTES + LB::BYTES, wave, C::BK);
+    wait_vmcnt<NDMA>();
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) fb0[j] = lb.frag_at(0, 0, j);
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) fa[i] = la.frag_at(0, 0, i);
+    wait_lgkmcnt<C::FM - 1>();
+
+    const int nk = (d.K + C::BK - 1) / C::BK;
+    const int P = (nk + 1) & ~1; // steps per tile (a step past K multiplies zeros)
+    for (;;) {
+        int b, tm, tn;
+        mfma_tile_of(t, tiles_m, tiles_n, group_m, b, tm, tn);
+        const int next = t + S;
+        Acc acc[C::FM][C::FN];
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+        // Step k loads k-tile k + 2; the last two steps (k = P - 2, P - 1) load the next tile's
+        // k-tiles 0 and 1.  The first step's wait for k-tile 1 also waits for the previous tile's
+        // stores (issued after those loads), which have had the step's first region to land.
+        for (int kt = 0; kt < P; kt += 2) {
+            const bool last = kt + 2 == P;
+            if (last) point(next);
+            const int k2 = last ? 0 : (kt + 2) * C::BK;
+            dma_kstep<C, 0>(0, k2, la, lb, fa, fb0, fb1, acc, LA0, LB0, wave);
+            dma_kstep<C, 0>(1, k2 + C::BK, la, lb, fa, fb0, fb1, acc, LA0, LB0, wave);
+        }
+        char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * (int64_t)dtype_size(d.dtype_c);
+        char* lw = E + wave * EPI;
+        const int ln = lane_here(), mrow0 = tm * C::BM + wm * C::WM, ncol0 = tn * C::BN + wn * C::WN;
+        if (d.dtype_c == TV_BFLOAT16) write_tile_staged<__bf16, C, Acc, EPI>(acc, lw, Cb, ln, mrow0, ncol0, d);
+        else write_tile_staged<_Float16, C, Acc, EPI>(acc, lw, Cb, ln, mrow0, ncol0, d);
+        if (next >= hi) break;
+        t = next;
+    }
+    // The last tile's zero-filling loads and its stores land before the workgroup ends.
+    wait_vmcnt<0>();
+}
+
+// Chained launch: one workgroup per CU walking several tiles.  Returns 1 if it did not launch:
+// fewer than two tiles per CU, or an output other than 16-bit with 16-byte aligned rows.
+template <class C>
+static int run_dma_chain(const GemmDesc& d, hipStream_t stream, int group_m, int tiles_m, int tiles_n, int64_t ntiles, int c_vec) {
+    if (c_vec != 2 || !(d.dtype_c == TV_BFLOAT16 || d.dtype_c == TV_FLOAT16)) return 1;
+    static int grid[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+    if (grid[dev] <= 0) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(gemm_dma_chain_kernel<C>), C::THREADS, 0) !=
+                hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
+            return 1;
+        grid[dev] = per_cu * cus;
+    }
+    const int G = grid[dev];
+    if (ntiles < 2 * (int64_t)G) return 1;
+    hipLaunchKernelGGL(gemm_dma_chain_kernel<C>, dim3((unsigned)G), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n, group_m, (int)ntiles);
+    return hipGetLastError();
+}
+
 // Stream-K launch of the direct-load kernel (one resident workgroup per CU: 128 KB of LDS) for few,
 // long tiles: at most a quarter as many 256x256 tiles as resident workgroups and K of at least 64
 // k-tiles.  A split 256x256 tile moves 256 KB per segment through the slots, which costs more than
@@ -862,6 +1011,11 @@ static int run_dma_cfg(const GemmDesc& d, hipStream_t stream, int group_m, bool 
             rc = run_dma_sk<C, false>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec);
         if (rc != 1) return rc;
     }
+    if constexpr (!__is_same(typename C::T, int8_t))
+        if (!epi) {
+            const int rc = run_dma_chain<C>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec);
+            if (rc != 1) return rc;
+        }
     if constexpr (!__is_same(typename C::T, int8_t))
         if (epi) {
             hipLaunchKernelGGL((gemm_dma_kernel<C, true>), dim3((unsigned)nwg), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,

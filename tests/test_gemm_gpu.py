@@ -296,6 +296,25 @@ def test_direct_load_stream_k_bit_exact(hip, dt, batch, M, K, N):
     np.testing.assert_array_equal(to_storage(plain), c)
 
 
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16])
+@pytest.mark.parametrize("batch,M,K,N", [(0, 4100, 520, 8200), (0, 4100, 100, 8200), (0, 4100, 50, 8200), (3, 2600, 700, 5000)])
+def test_direct_load_chain_exact(hip, dt, batch, M, K, N):
+    """16-bit GEMMs of at least two 256x256 tiles per CU run the chained persistent kernel (each
+    workgroup's k-loop runs on into its next tile, whose first two k-tiles load during the
+    previous tile's last steps and store): 561 tiles with ragged M, N and K (9 k-tiles, an odd
+    count), K of two and of one k-tile, and 660 tiles over a batch with per-batch B.
+    Integer-valued inputs in [-2, 2]: the fp32 sums are exact in any order, so the output is each
+    exact sum rounded once; a second call gives the same bits."""
+    lead = (batch,) if batch else ()
+    x = ints(16, lead + (M, K), -2, 2)
+    y = ints(17, lead + (K, N), -2, 2)
+    ta, tb = to_torch(half_bits(x, dt), dt), to_torch(half_bits(y, dt), dt)
+    exact = np.matmul(x, y)  # fp32 BLAS: integer partial sums below 2^24, exact in any order
+    c = to_storage(hip.gemm(ta, tb))
+    np.testing.assert_array_equal(c, half_bits(exact, dt))
+    np.testing.assert_array_equal(to_storage(hip.gemm(ta, tb)), c)
+
+
 # ---- views, offsets, batches ----------------------------------------------------------------
 
 @pytest.mark.parametrize("dt", [FLOAT32, BFLOAT16, INT8])
