@@ -18,6 +18,8 @@ sample of each workload.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c2,...] [--no-cpu]
                        [--only c2]   (only that config's kernel, e.g. under rocprofv3)
                        [--vendor]    (also time torch's own library GEMM on the same inputs)
+       python bench.py --trace-summary kernel_trace.csv --steps K
+                       (per-configuration kernel durations of a rocprofv3 trace of this bench)
 """
 from __future__ import annotations
 
@@ -90,11 +92,24 @@ DTYPE = {"c1": "fp32", "c2": "int8", "c3": "bf16", "c3_fused": "bf16", "c4": "fp
 KERNEL = {
     "c1": "gemm_mfma_sk_kernel<GemmCfg<float, 128, 128, 2, 2, 0, 1>, false> (stream-K schedule)",
     "c2": "gemm_dma_kernel<GemmCfg<signed char, 256, 256, 2, 4, 0, 1>, false>",
-    "c3": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, false>",
+    "c3": "gemm_dma_chain_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>> (chained tiles)",
     "c3_fused": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, true>",
     "c4": "gemm_smallk_kernel<GemmCfg<_Float16, 256, 256, 2, 4, 0, 0>>",
     "c5m1": "gemv_mfma_kernel<__bf16, 4, 2>",
     "c5m8": "gemv_mfma_kernel<__bf16, 4, 2>",
+}
+# The same kernels as they appear in a rocprofv3 kernel trace (demangled, or mangled where the
+# profiler's demangler gives up on __bf16 / _Float16 template arguments).
+TRACE_KERNEL = {
+    "c1": r"gemm_mfma_sk_kernel.*(GemmCfg<float, 128, 128|GemmCfgIfLi128ELi128E)",
+    "c2": r"gemm_dma_kernel.*(GemmCfg<signed char, 256, 256|GemmCfgIaLi256ELi256E)",
+    "c3": r"gemm_dma_chain_kernel.*(GemmCfg<__bf16|GemmCfgIDF16b)",
+    "c3_fused": r"gemm_dma_kernel.*(GemmCfg<__bf16|GemmCfgIDF16b).*(true|Lb1E)",
+    "c4": r"gemm_smallk_kernel.*(GemmCfg<_Float16|GemmCfgIDF16_)",
+    "c5m1": r"gemv_mfma_kernel.*(__bf16|DF16b)",
+    "c5m8": r"gemv_mfma_kernel.*(__bf16|DF16b)",
+    "cast_c3a": r"cast_kernel", "random_c3a": r"random_kernel", "fill_c3a": r"fill_kernel",
+    "transpose_c4k": r"repack_transpose16_kernel",
 }
 # Bound each configuration is judged against (c4's arithmetic intensity, 113.8 FLOP/B, is below
 # the fp16 ridge of about 315: HBM-bound).
@@ -406,6 +421,44 @@ def trace_check(name: str, res: dict) -> dict | None:
     return out
 
 
+def trace_summary(csv_path: str, steps: int) -> dict:
+    """Per-configuration durations (End - Start) of the last `steps` dispatches of each
+    configuration's kernel in a rocprofv3 kernel_trace.csv of `bench.py --steps S --no-cpu`: the
+    timed launches close each configuration's run of back-to-back dispatches.  A kernel's dispatches
+    are cut into runs at gaps of more than 2 ms; configurations that share a kernel (c5 M=1, then
+    M=8) take its runs in order, the others its longest run."""
+    import csv
+    import re
+    import statistics as st
+    rows = sorted(csv.DictReader(open(csv_path)), key=lambda r: int(r["Start_Timestamp"]))
+    out, used = {}, {}
+    for name, pat in TRACE_KERNEL.items():
+        rx = re.compile(pat)
+        ds = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in rows if rx.search(r["Kernel_Name"])]
+        runs, cur = [], []
+        for d in ds:
+            if cur and d[0] - cur[-1][1] > 2_000_000:
+                runs.append(cur)
+                cur = []
+            cur.append(d)
+        if cur:
+            runs.append(cur)
+        runs = [r for r in runs if len(r) >= steps]
+        if not runs:
+            continue
+        if pat in used:
+            i = used[pat] + 1
+        else:
+            i = 0 if name == "c5m1" else max(range(len(runs)), key=lambda j: len(runs[j]))
+        if i >= len(runs):
+            continue
+        used[pat] = i
+        dur = [e - b for b, e in runs[i][-steps:]]
+        out[name] = {"dispatches": len(dur), "avg_ns": st.mean(dur), "median_ns": st.median(dur),
+                     "min_ns": min(dur), "max_ns": max(dur), "run_dispatches": len(runs[i])}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -416,7 +469,12 @@ def main() -> int:
                     help="run only this config's GPU kernel (for profilers); 'copy' runs the traffic calibration copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--vendor", action="store_true", help="also time torch's library GEMM on the same inputs")
+    ap.add_argument("--trace-summary", metavar="CSV", default=None,
+                    help="summarise a rocprofv3 kernel_trace.csv of this bench (with the same --steps) and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(json.dumps({"steps": args.steps, "configs": trace_summary(args.trace_summary, args.steps)}, indent=1))
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the matmul path would shard by batch/M or N columns with no exchange, which is not "

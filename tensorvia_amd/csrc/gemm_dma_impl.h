@@ -978,6 +978,8 @@ static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int ti
     SkArgs sk;
     sk.iters = iters;
     sk.nk = nk;
+    sk.dp_tiles = 0; // every tile is split here (at most a quarter as many tiles as workgroups)
+    sk.wgs = G;
     const int rc = gemm_sk_workspace(stream, (size_t)ntiles, (size_t)2 * G * sk_slot_bytes<C>(), &sk.cnt, &sk.slots);
     if (rc) return rc;
     hipLaunchKernelGGL((gemm_dma_sk_kernel<C, FUSED>), dim3((unsigned)G), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n, group_m,

@@ -728,19 +728,24 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
 }
 
 // ---------------------------------------------------------------------------------------------
-// Stream-K schedule (fp32): G resident workgroups take equal contiguous ranges of the (tile, k-tile)
-// iteration space instead of one workgroup per tile.  Every CU then does the same work however the
-// tiles divide over the CUs (c1: 672 tiles of 128x128 on 256 CUs, 2.625 per CU, which the
-// one-per-tile launch runs in the time of 3), and fewer tiles than CUs still use every CU.  Workgroup w owns iterations
-// [w*I/G, (w+1)*I/G); a tile cut by a range boundary is computed in segments by consecutive
-// workgroups.  Each segment stores its accumulators in a slot (register order, 16 bytes a lane),
+// Stream-K schedule (fp32): G resident workgroups share the work instead of one workgroup per
+// tile.  Every CU then does the same work however the tiles divide over the CUs (c1: 672 tiles of
+// 128x128 on 256 CUs, 2.625 per CU, which the one-per-tile launch runs in the time of 3), and fewer
+// tiles than CUs still use every CU.  Whole rounds of G tiles run whole (workgroup w takes tiles
+// w, w + G, ...), so the workgroups running side by side take neighbouring tiles at the same k and
+// share their operands in L2; the last, partial round is split: the first `wgs` workgroups take
+// equal contiguous ranges of its (tile, k-tile) iteration space, workgroup w iterations
+// [w*I/wgs, (w+1)*I/wgs), and a tile cut by a range boundary is computed in segments by
+// consecutive workgroups.  Each segment stores its accumulators in a slot (register order, 16 bytes a lane),
 // counts itself in (publish_and_count), and the last segment to arrive sums the slots in segment
 // order (deterministic) and writes the tile.  Workgroup w's slots: 2w for the segment that continues
 // a tile begun before its range, 2w + 1 for the one that begins a tile that runs past it (a range
 // holds at most one of each).  No workgroup waits for another.
 struct SkArgs {
-    int64_t iters; // tiles x k-tiles
+    int64_t iters; // split tiles x k-tiles
     int nk;        // k-tiles per tile
+    int dp_tiles;  // tiles [0, dp_tiles) run whole, workgroup w taking w, w + G, ...; the rest split
+    int wgs;       // workgroups sharing the split tiles' iterations (the first wgs, at most G)
     int* cnt;      // [tiles] arrival counters, zero between launches
     char* slots;   // [2 x workgroups][slot bytes]
 };
@@ -760,19 +765,40 @@ void gemm_mfma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int 
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int G = gridDim.x;
     int w = blockIdx.x;
-    if ((G & 7) == 0) w = (w & 7) * (G >> 3) + (w >> 3); // consecutive ranges on one XCD
-    const int64_t I = sk.iters;
+    if ((gridDim.x & 7) == 0) w = (w & 7) * (gridDim.x >> 3) + (w >> 3); // consecutive ids on one XCD
     const int nk = sk.nk;
+
+    // Whole tiles first, in the grouped tile order: the workgroups side by side on an XCD take
+    // neighbouring tiles and start them together, so they share A and B k-slices in its L2.
+    for (int tile = w; tile < sk.dp_tiles; tile += (int)gridDim.x) {
+        int b, tm, tn;
+        mfma_tile_of(tile, tiles_m, tiles_n, group_m, b, tm, tn);
+        const int m0 = tm * C::BM, n0 = tn * C::BN;
+        Acc acc[C::FM][C::FN];
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+        lds_barrier(); // the previous tile's epilogue is done with the LDS
+        mfma_tile_kloop<C>(d, smem, b, m0, n0, 0, nk, acc);
+        mfma_tile_store<C, FUSED>(d, smem, b, m0, n0, c_vec, acc);
+    }
+
+    // Then the split tiles [dp_tiles, tiles): the first sk.wgs workgroups take equal ranges of their
+    // iterations.
+    const int G = sk.wgs;
+    if (w >= G) return;
+    const int64_t I = sk.iters;
     const int64_t it_end = (int64_t)(w + 1) * I / G;
     // The workgroup whose range holds iteration it: the largest v with floor(v * I / G) <= it.
     auto owner = [&](int64_t it) { return (int)(((it + 1) * G - 1) / I); };
     auto slot_rsrc = [&](int slot) { return make_rsrc(sk.slots + (int64_t)slot * SLOT, SLOT); };
 
     for (int64_t it = (int64_t)w * I / G; it < it_end;) {
-        const int tile = (int)(it / nk);
-        const int kt0 = (int)(it - (int64_t)tile * nk);
+        const int rel = (int)(it / nk); // split tile index; its k-tiles are iterations rel*nk ..
+        const int tile = sk.dp_tiles + rel;
+        const int kt0 = (int)(it - (int64_t)rel * nk);
         const int kt1 = (int)min((int64_t)nk, kt0 + (it_end - it));
         it += kt1 - kt0;
         int b, tm, tn;
@@ -786,7 +812,7 @@ void gemm_mfma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int 
         lds_barrier(); // the previous segment's epilogue is done with the LDS
         mfma_tile_kloop<C>(d, smem, b, m0, n0, kt0, kt1, acc);
         if (kt0 != 0 || kt1 != nk) {
-            const int64_t t0 = (int64_t)tile * nk;
+            const int64_t t0 = (int64_t)rel * nk;
             const int first = owner(t0), last = owner(t0 + nk - 1);
             {
                 const __amdgpu_buffer_rsrc_t r = slot_rsrc(w == first ? 2 * w + 1 : 2 * w);
@@ -870,12 +896,17 @@ static int run_cfg_sk(const GemmDesc& d, hipStream_t stream, int group_m, int ti
     int G = sk_grid<C>();
     if (G <= 0) return 1;
     if (nk < 32 && ntiles >= G / 2) return 1; // G / 2: about one tile per CU
-    const int64_t iters = ntiles * nk;
-    if (iters / 8 < G) G = (int)(iters / 8);
+    // Whole rounds of G tiles run whole; only the last, partial round is split.
+    const int64_t dp = ntiles > G ? ntiles / G * G : 0;
+    const int64_t iters = (ntiles - dp) * nk;
+    const int wgs = (int)(iters / 8 < G ? iters / 8 : G);
+    if (dp == 0) G = wgs;
     if (G < 1) return 1;
     SkArgs sk;
     sk.iters = iters;
     sk.nk = nk;
+    sk.dp_tiles = (int)dp;
+    sk.wgs = wgs;
     const int rc = gemm_sk_workspace(stream, (size_t)ntiles, (size_t)2 * G * sk_slot_bytes<C>(), &sk.cnt, &sk.slots);
     if (rc) return rc;
     hipLaunchKernelGGL((gemm_mfma_sk_kernel<C, FUSED>), dim3((unsigned)G), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,

@@ -136,11 +136,14 @@ def test_fp32_uniform_vs_oracle(hip, shape):
 
 
 @pytest.mark.parametrize("batch,M,K,N", [(0, 2592, 2048, 4096), (0, 1300, 1024, 4100), (2, 1000, 1056, 2100),
-                                         (0, 1700, 1056, 2900), (0, 300, 264, 500)])
+                                         (0, 1700, 1056, 2900), (0, 300, 264, 500), (0, 4096, 1024, 4096),
+                                         (0, 4400, 1024, 4096)])
 def test_fp32_stream_k_bit_exact(hip, batch, M, K, N):
     """fp32 GEMMs on the stream-K schedule, whose tiles are summed in segments by several
-    workgroups: c1 (672 tiles, 2.625 per CU); 363, 272 and 322 tiles with ragged M/N tails and a
-    batch (K of 32 and 33 k-tiles); 12 tiles at K = 9 k-tiles (fewer tiles than CUs).  Integer-valued
+    workgroups: c1 (672 tiles, 2.625 per CU: one round of whole tiles, then 160 split); 363, 272 and
+    322 tiles with ragged M/N tails and a batch (K of 32 and 33 k-tiles); 12 tiles at K = 9 k-tiles
+    (fewer tiles than CUs); 1024 tiles (two whole rounds, nothing split) and 1120 (two rounds, then
+    96 tiles split over fewer workgroups than are resident).  Integer-valued
     inputs make every order exact: bit-exact against exact sums, equal to the plain kernel
     (tv_hip_gemm_noalloc takes no workspace, hence no stream-K), and equal on a second call."""
     lead = (batch,) if batch else ()
