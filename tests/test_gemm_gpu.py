@@ -318,6 +318,22 @@ def test_direct_load_chain_exact(hip, dt, batch, M, K, N):
     np.testing.assert_array_equal(to_storage(hip.gemm(ta, tb)), c)
 
 
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16])
+@pytest.mark.parametrize("a_t,b_t", [(True, False), (False, True), (True, True)], ids=["At", "Bt", "AtBt"])
+def test_direct_load_chain_transposed_views(hip, dt, a_t, b_t):
+    """The chained kernel with the other operand layouts, as transposed views consumed through their
+    strides (A M-contiguous, B K-contiguous, or both; every pitch a whole number of 16-byte chunks,
+    so both stay on the direct-load kernels): 561 tiles, ragged M/N, K = 328 (6 k-tiles).
+    Integer-valued inputs, exact sums rounded once."""
+    M, K, N = 4104, 328, 8200
+    x = ints(18, (M, K), -2, 2)
+    y = ints(19, (K, N), -2, 2)
+    ta = to_torch(half_bits(np.ascontiguousarray(x.T), dt), dt).t() if a_t else to_torch(half_bits(x, dt), dt)
+    tb = to_torch(half_bits(np.ascontiguousarray(y.T), dt), dt).t() if b_t else to_torch(half_bits(y, dt), dt)
+    c = to_storage(hip.gemm(ta, tb))
+    np.testing.assert_array_equal(c, half_bits(np.matmul(x, y), dt))
+
+
 # ---- views, offsets, batches ----------------------------------------------------------------
 
 @pytest.mark.parametrize("dt", [FLOAT32, BFLOAT16, INT8])
