@@ -342,7 +342,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
     __shared__ Acc red[WAVES][8][NB];
     __shared__ int last_flag;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // The wave index from the first lane: wave-uniform to the compiler, so the loop below has scalar
+    // control flow.  With a per-lane index the per-chunk guard became an exec-mask branch, and the
+    // compiler waited for every load of the next chunk inside each chunk (one chunk in flight, not
+    // DEPTH) and moved the accumulators between register files every chunk.
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lin = xcd_remap(blockIdx.x, gridDim.x);
     const int b = lin / g.nblk;
     const int n0 = (lin - b * g.nblk) * NB;
@@ -352,6 +356,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
     const int nch = (ks + CH - 1) / CH;
     const int kpad = nch * CH;
     const int niter = (nch - wave + WAVES - 1) / WAVES; // chunks wave, wave + WAVES, ...
+    const int nsteps = (niter + DEPTH - 1) / DEPTH * DEPTH; // the loop's count: chunks past niter are zeros
 
     const int64_t rowb = d.sb_k * ES;
     const char* wbase = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)k0 * d.sb_k) * ES;
@@ -398,16 +403,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
     const int rd_off = ES == 2 ? (kb + (fr >> 2)) * PITCH + 8 * (fr & 3) : (kb + (fr >> 1)) * PITCH + 8 * (fr & 1);
     const bool arow = fr < 8;
     const char* xa = xs + (lane & 7) * kpad * ES + kb * ES;
-    for (int j0 = 0; j0 < niter; j0 += DEPTH) {
+    // No per-chunk guard: the step count is a multiple of DEPTH, and a chunk past niter multiplies
+    // zeros (its W loads are out of range, its x fragment is zeroed).
+    for (int j0 = 0; j0 < nsteps; j0 += DEPTH) {
 #pragma unroll
         for (int dd = 0; dd < DEPTH; ++dd) {
             const int j = j0 + dd;
-            if (j < niter) {
+            {
                 const int c = wave + WAVES * j;
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) *reinterpret_cast<u32x4*>(wl + wr_off + q * 8 * PITCH) = w[dd][q];
-                u32x4 a = *reinterpret_cast<const u32x4*>(xa + c * CH * ES);
-                if (!arow) a = u32x4{0, 0, 0, 0};
+                u32x4 a = *reinterpret_cast<const u32x4*>(xa + (j < niter ? c : 0) * CH * ES);
+                if (!arow || j >= niter) a = u32x4{0, 0, 0, 0};
 #pragma unroll
                 for (int f = 0; f < NF; ++f) {
                     const lds_char* p = (const lds_char*)(wl + rd_off + f * 16 * ES);
@@ -424,7 +431,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
                     }
                     Mfma<T>::run(a, bf, acc[f]);
                 }
-                if (j + DEPTH < niter) issue(dd, j + DEPTH);
+                issue(dd, j + DEPTH); // out of range past niter: zeros
             }
         }
     }
