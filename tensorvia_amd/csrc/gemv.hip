@@ -379,15 +379,26 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
 #pragma unroll
     for (int j = 0; j < DEPTH; ++j) issue(j, j);
 
-    // x[b][0..8)[k0 .. k0 + kpad) in LDS; rows >= M and columns >= ks are zero.
+    // x[b][0..8)[k0 .. k0 + kpad) in LDS; rows >= M and columns >= ks are zero.  Four chunks per
+    // thread are loaded before any is stored: each wait for an x load also waits for the W loads
+    // issued before it, so the loads go out together and pay that wait once.
     {
         const char* xb = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + k0) * ES;
         const int cpr = kpad * ES / 16;
-        for (int i = tid; i < 8 * cpr; i += THREADS) {
-            const int m = i / cpr, c = i - m * cpr;
-            u32x4 v = {0, 0, 0, 0};
-            if (m < d.M && c * 16 < ks * ES) v = *reinterpret_cast<const u32x4*>(xb + (int64_t)m * d.sa_m * ES + c * 16);
-            *reinterpret_cast<u32x4*>(xs + m * kpad * ES + c * 16) = v;
+        for (int i0 = tid; i0 < 8 * cpr; i0 += 4 * THREADS) {
+            u32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * THREADS, m = i / cpr, c = i - m * cpr;
+                v[u] = u32x4{0, 0, 0, 0};
+                if (i < 8 * cpr && m < d.M && c * 16 < ks * ES)
+                    v[u] = *reinterpret_cast<const u32x4*>(xb + (int64_t)m * d.sa_m * ES + c * 16);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * THREADS;
+                if (i < 8 * cpr) *reinterpret_cast<u32x4*>(xs + i * 16) = v[u];
+            }
         }
     }
     __syncthreads();
