@@ -129,10 +129,10 @@ int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_st
  * forbid hipMalloc).  Same arguments and routing as tv_hip_gemm.  The split-K partials of the
  * M <= 8 GEMV kernels come from a static device array of 4 MiB of partial slots plus 16,384 arrival
  * counters per GPU, held until the process ends, instead of tv_hip_gemm's workspace.  GEMMs
- * (M > 8) run one workgroup per tile instead of tv_hip_gemm's stream-K schedule, whose partial
- * tiles need a workspace, so fp32 and 16-bit results of shapes that tv_hip_gemm runs stream-K
- * can differ from its results in the last bits (summation order); every other call, and every
- * int8 call, gives tv_hip_gemm's results bit for bit.  A call whose split needs more returns
+ * (M > 8) that tv_hip_gemm splits with its stream-K schedule, whose partial tiles need a
+ * workspace, run unsplit here, so their fp32 and 16-bit results can differ from tv_hip_gemm's in
+ * the last bits (summation order); every other call, and every int8 call, gives tv_hip_gemm's
+ * results bit for bit.  A call whose split needs more returns
  * TV_E_SCRATCH (e.g. M = 8 bf16 needs 2 KiB per (64-column strip, K-slice) pair: c5's
  * x[8,4096] @ W[4096,11008] needs 1.4 MiB).
  * The first call on a GPU looks the array up (hipGetSymbolAddress) and clears its counters with a
