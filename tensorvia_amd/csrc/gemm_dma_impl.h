@@ -327,13 +327,11 @@ template <class C> constexpr int dma_lds_bytes() {
 // One k-tile of the direct-load pipeline for one wave.  Stage `cs` holds k-tile t, whose k-group 0
 // is already in fa / fb0; stage 1 - cs holds k-tile t + 1 once the barrier has passed.
 //   Region 1: rows on k-group 0; after row i reload fa[i] with k-group 1 and read fb1[i].
-//   Wait until at most VMW vector-memory operations of this wave are in flight, i.e. tile t + 1's
-//   loads have landed when exactly VMW operations were issued after them (0 here; stores issued
-//   after them for a caller that passes their count), barrier (tile t + 1 visible, stage cs
-//   free).
+//   Wait for this wave's vector-memory operations (tile t + 1's loads, and anything issued before
+//   them), barrier (tile t + 1 visible, stage cs free).
 //   Region 2: rows on k-group 1; one load of the k-tile at k offset k2 into stage cs per row;
 //   after row i reload fa[i] with k-group 0 of tile t + 1 and read its fb0[i].
-template <class C, int VMW, class LA, class LB, class Acc>
+template <class C, class LA, class LB, class Acc>
 __device__ __attribute__((always_inline)) inline void dma_kstep(int cs, int k2, const LA& la, const LB& lb, u32x4 (&fa)[C::FM],
                                                                 u32x4 (&fb0)[C::FN], u32x4 (&fb1)[C::FN], Acc (&acc)[C::FM][C::FN],
                                                                 unsigned LA0, unsigned LB0, int wave) {
@@ -371,7 +369,7 @@ __device__ __attribute__((always_inline)) inline void dma_kstep(int cs, int k2, 
     sched_rows();
     const __amdgpu_buffer_rsrc_t ra = la.rsrc(k2);
     const __amdgpu_buffer_rsrc_t rb = lb.rsrc(k2);
-    wait_vmcnt<VMW>();
+    wait_vmcnt<0>();
     dma_barrier();
     const unsigned sa = LA0 + (unsigned)(cs * LA::BYTES), sb = LB0 + (unsigned)(cs * LB::BYTES);
 #pragma unroll
@@ -424,7 +422,7 @@ __device__ __attribute__((always_inline)) inline void dma_tile_kloop(const GemmD
     u32x4 fa[C::FM], fb0[C::FN], fb1[C::FN];
     constexpr int NDMA = LA::PER_WAVE + LB::PER_WAVE;
     auto step = [&](int cs, int kt) {
-        dma_kstep<C, 0>(cs, (kt + 2) * C::BK, la, lb, fa, fb0, fb1, acc, LA0, LB0, wave);
+        dma_kstep<C>(cs, (kt + 2) * C::BK, la, lb, fa, fb0, fb1, acc, LA0, LB0, wave);
     };
 
     // Prologue: k-tiles kt0 and kt0 + 1 in flight, then k-group 0 of kt0.
@@ -909,8 +907,8 @@ void gemm_dma_chain_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, in
             const bool last = kt + 2 == P;
             if (last) point(next);
             const int k2 = last ? 0 : (kt + 2) * C::BK;
-            dma_kstep<C, 0>(0, k2, la, lb, fa, fb0, fb1, acc, LA0, LB0, wave);
-            dma_kstep<C, 0>(1, k2 + C::BK, la, lb, fa, fb0, fb1, acc, LA0, LB0, wave);
+            dma_kstep<C>(0, k2, la, lb, fa, fb0, fb1, acc, LA0, LB0, wave);
+            dma_kstep<C>(1, k2 + C::BK, la, lb, fa, fb0, fb1, acc, LA0, LB0, wave);
         }
         char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * (int64_t)dtype_size(d.dtype_c);
         char* lw = E + wave * EPI;
