@@ -91,9 +91,13 @@ struct DmaOperand {
     static constexpr int RB = ROWS * ES;           // M/N layout: bytes per k row
     static constexpr int CPR = RB / 16;            // M/N layout: chunks per k row
     static constexpr int KRB = 1024 / RB;          // M/N layout: k rows per block
+    // M/N layout: LDS bytes between the k-groups of a k-tile (64 int8 / 32 16-bit k rows) and
+    // between the two transposed reads of a fragment (8 / 4 k rows).
+    static constexpr int KGB = (ES == 1 ? 64 : 32) * RB;
+    static constexpr int RD2 = (ES == 1 ? 8 : 4) * RB;
     static_assert(NBLK % NWAVES == 0, "load blocks must divide over the waves");
-    static_assert(MODE == LOAD_KCONTIG || (MODE == LOAD_MNCONTIG && ES <= 2 && RB == 256 * ES && ROWS == 256),
-                  "M/N layout is laid out for 256-row int8 / 16-bit tiles");
+    static_assert(MODE == LOAD_KCONTIG || (MODE == LOAD_MNCONTIG && ES <= 2 && (ROWS == 256 || (ES == 2 && ROWS == 128))),
+                  "M/N layout is laid out for 256-row int8 / 16-bit and 128-row 16-bit tiles");
 
     const char* base; // element (row0, k = 0) of this tile, as bytes
     int64_t s_r, s_k; // element strides
@@ -179,7 +183,9 @@ struct DmaOperand {
     //  M/N layout: chunk (q0 + step f) ^ swz(kr) = (q0 ^ swz(kr)) ^ (step f) because q0 has no bits
     //              below the fragment count times `step`; swz is the same for both reads of a lane
     //              (k rows kr and kr + 8 / kr + 4) and both k-groups (kr + 64 / kr + 32), so
-    //              address = (xf ^ (f << FSH)) + 16384 kg + 2048 (second read).
+    //              address = (xf ^ (f << FSH)) + KGB kg + RD2 (second read).  A k row's bytes (RB,
+    //              256 or 512) are a whole multiple of the 64 banks, so the swizzle spreads the
+    //              rows of a transposed read over the banks the same way for either.
     unsigned xf;
     static constexpr int FSH = ES == 1 ? 4 : 5;
     __device__ inline void xinit(unsigned op_base, int lane, int w0) {
@@ -201,14 +207,14 @@ struct DmaOperand {
             const lds_char* p = (const lds_char*)(uintptr_t)(xf ^ (unsigned)(kg << 6)) + st * BYTES + f * 2048;
             return *(const __attribute__((address_space(3))) u32x4*)p;
         } else {
-            const lds_char* p = (const lds_char*)(uintptr_t)(xf ^ (unsigned)(f << FSH)) + st * BYTES + kg * 16384;
+            const lds_char* p = (const lds_char*)(uintptr_t)(xf ^ (unsigned)(f << FSH)) + st * BYTES + kg * KGB;
             if constexpr (ES == 1) {
                 const i32x2_t a = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
-                const i32x2_t b = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(p + 2048));
+                const i32x2_t b = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(p + RD2));
                 return u32x4{(unsigned)a.x, (unsigned)a.y, (unsigned)b.x, (unsigned)b.y};
             } else {
                 const i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
-                const i16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 2048));
+                const i16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + RD2));
                 const uint2 l2 = __builtin_bit_cast(uint2, a), h2 = __builtin_bit_cast(uint2, b);
                 return u32x4{l2.x, l2.y, h2.x, h2.y};
             }
@@ -318,6 +324,11 @@ __device__ inline void write_tile_wg_i8(const i32x4 (&acc)[C::FM][C::FN], char* 
     }
 }
 
+// Waves per SIMD the direct-load kernels' registers must allow: two for the 256x256 tile (8
+// waves a workgroup, one workgroup per CU); four for the 128x128 tile (8 waves of 64x32, 64 KB of
+// LDS, so two workgroups per CU).
+template <class C> constexpr int dma_waves_per_eu() { return C::BM * C::BN <= 128 * 128 ? 4 : C::THREADS / 256; }
+
 // LDS of the direct-load kernels: [A stage 0 | A stage 1 | B stage 0 | B stage 1]; the epilogue
 // reuses all of it.
 template <class C> constexpr int dma_lds_bytes() {
@@ -401,7 +412,7 @@ __device__ __attribute__((always_inline)) inline void dma_tile_kloop(const GemmD
     const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
     const unsigned LA0 = (unsigned)(uintptr_t)(lds_void*)L;
     const unsigned LB0 = LA0 + 2 * LA::BYTES;
-    static_assert(LA::BYTES + 16384 + 2048 < 65536 && LB::BYTES + 16384 + 2048 < 65536 &&
+    static_assert(LA::BYTES + LA::KGB + LA::RD2 < 65536 && LB::BYTES + LB::KGB + LB::RD2 < 65536 &&
                       LA::BYTES + (C::FM - 1) * 2048 < 65536 && LB::BYTES + (C::FN - 1) * 2048 < 65536,
                   "stage 1 and fragment offsets must fit a ds_read immediate");
     const int K_eff = min(d.K, kt1 * C::BK);
@@ -526,7 +537,7 @@ __device__ __attribute__((always_inline)) inline void dma_tile_store(const GemmD
 
 template <class C, bool FUSED = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
-                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
+                          amdgpu_waves_per_eu(dma_waves_per_eu<C>(), dma_waves_per_eu<C>())))
 void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec) {
     using Acc = typename Mfma<typename C::T>::Acc;
     __shared__ __attribute__((aligned(1024))) char L[dma_lds_bytes<C>()];
@@ -550,7 +561,7 @@ void gemm_dma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_ve
 // and hand-over; int32 accumulators of int8 sum exactly in any order).
 template <class C, bool FUSED = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
-                          amdgpu_waves_per_eu(C::THREADS / 256, C::THREADS / 256)))
+                          amdgpu_waves_per_eu(dma_waves_per_eu<C>(), dma_waves_per_eu<C>())))
 void gemm_dma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_vec, SkArgs sk) {
     using Acc = typename Mfma<typename C::T>::Acc;
     constexpr int SLOT = sk_slot_bytes<C>();
@@ -944,15 +955,15 @@ static int run_dma_chain(const GemmDesc& d, hipStream_t stream, int group_m, int
     return hipGetLastError();
 }
 
-// Stream-K launch of the direct-load kernel (one resident workgroup per CU: 128 KB of LDS) for few,
-// long tiles: at most a quarter as many 256x256 tiles as resident workgroups and K of at least 64
-// k-tiles.  A split 256x256 tile moves 256 KB per segment through the slots, which costs more than
-// the balance gains once the tiles are many.  Measured (settled clocks, same box, against one
-// workgroup per tile): bf16 [512,8192]@[8192,8192] 88.9 against 146.7 us, [128,8192]@[8192,8192]
-// 80.6 against 145 us, [1024,4096]@[4096,4096] 62.0 against 77.3 us; int8 [512,8192]@[8192,8192]
-// 52.0 against 75.5 us; but 192 tiles (M = 3000, K = 4096) 121.5 against 83.0 us in bf16, and 128
-// tiles slower too.  c2 (256 tiles) and c3 (2048) keep one workgroup per tile.  Returns 1 if it did
-// not launch.
+// Stream-K launch of the direct-load kernel for few, long tiles: at most a quarter as many tiles as
+// resident workgroups and K of at least 64 k-tiles.  A split tile moves its fp32 partial sums
+// through the slots once per segment, which costs more than the balance gains once the tiles are
+// many.  Measured (settled clocks, same box, against one workgroup per tile) on int8 256x256 tiles
+// (one resident per CU): [512,8192]@[8192,8192] 52.0 against 75.5 us; and on bf16 256x256 tiles
+// before 16-bit GEMMs this small moved to 128x128 tiles: [512,8192]@[8192,8192] 88.9 against
+// 146.7 us, but 192 tiles (M = 3000, K = 4096) 121.5 against 83.0 us.  bf16 [128,8192]@[8192,8192]
+// (64 tiles of 128x128, two resident per CU) runs 43.5 us split.  c2 (256 tiles) and c3 (2048)
+// keep one workgroup per tile.  Returns 1 if it did not launch.
 template <class C, bool FUSED>
 static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int tiles_m, int tiles_n, int64_t ntiles, int c_vec) {
     const int nk = (d.K + C::BK - 1) / C::BK;
@@ -1003,15 +1014,17 @@ static int run_dma_cfg(const GemmDesc& d, hipStream_t stream, int group_m, bool 
     const bool epi = d.bias != nullptr || d.act != TV_ACT_NONE;
     if (epi && d.sc_n != 1) return TV_E_UNSUPPORTED; // the fused store writes rows of C
     if (may_alloc) {
+        // 16-bit GEMMs few enough to split (at most a quarter as many 256x256 tiles as CUs) always
+        // take 128x128 tiles in run_modes_dma, so the 256x256 16-bit configurations never split.
         int rc = 1;
-        if constexpr (!__is_same(typename C::T, int8_t))
+        if constexpr (__is_same(typename C::T, int8_t))
+            rc = run_dma_sk<C, false>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec);
+        else if constexpr (C::BM == 128)
             rc = epi ? run_dma_sk<C, true>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec)
                      : run_dma_sk<C, false>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec);
-        else
-            rc = run_dma_sk<C, false>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec);
         if (rc != 1) return rc;
     }
-    if constexpr (!__is_same(typename C::T, int8_t))
+    if constexpr (!__is_same(typename C::T, int8_t) && C::BM == 256)
         if (!epi) {
             const int rc = run_dma_chain<C>(d, stream, group_m, tiles_m, tiles_n, nwg, c_vec);
             if (rc != 1) return rc;
@@ -1055,6 +1068,18 @@ static bool smallk_ok(const GemmDesc& d, int es, int bm_rows, int bn_rows) {
     return tiles >= 1024;
 }
 
+// Compute units of the current device (cached per device; 256 if the runtime cannot tell).
+static int device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] <= 0) {
+        int cus = 0;
+        cached[dev] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0 ? cus : 256;
+    }
+    return cached[dev];
+}
+
 // 16-bit / int8 inputs: direct-to-LDS kernel for the vector layouts, gemm_mfma_kernel otherwise.
 template <typename T, int BM, int BN, int WMW, int WNW>
 static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m, bool may_alloc) {
@@ -1071,6 +1096,24 @@ static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m, boo
         TV_CASE(LOAD_MNCONTIG, LOAD_MNCONTIG)
         TV_CASE(LOAD_MNCONTIG, LOAD_KCONTIG)
 #undef TV_CASE
+    }
+    // 16-bit GEMMs whose 128x128 tiles all fit one round of resident workgroups (two per CU) run
+    // 128x128 tiles: few 256x256 tiles leave CUs idle.  Measured against 256x256 tiles (and their
+    // stream-K schedule) on one box: bf16 [1024,4096]@[4096,4096] 45.5 against 62.7 us,
+    // [128,8192]@[8192,8192] 43.5 against 79.3, [2048]^3 25.6 against 41.6, [2048,4096]@[4096,4096]
+    // 67.4 against 78.6 (512 tiles of 128x128); but [3000,4096]@[4096,4096] (768 of them) 102.6
+    // against 83.7.
+    if constexpr (sizeof(T) == 2 && BM == 256 && BN == 256) {
+        const int64_t tiles128 = (int64_t)((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
+        if (am != LOAD_GENERIC && bm != LOAD_GENERIC && tiles128 <= 2 * (int64_t)device_cus()) {
+#define TV_CASE(A_, B_) \
+    if (am == A_ && bm == B_) return run_dma_cfg<GemmCfg<T, 128, 128, 2, 4, A_, B_>>(d, stream, group_m, may_alloc);
+            TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)
+            TV_CASE(LOAD_KCONTIG, LOAD_KCONTIG)
+            TV_CASE(LOAD_MNCONTIG, LOAD_MNCONTIG)
+            TV_CASE(LOAD_MNCONTIG, LOAD_KCONTIG)
+#undef TV_CASE
+        }
     }
 #define TV_CASE(A_, B_) \
     if (am == A_ && bm == B_) return run_dma_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream, group_m, may_alloc);

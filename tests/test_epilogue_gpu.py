@@ -10,7 +10,7 @@ widened by the activation's slope (at most 1; the float exp/tanh add a few ulp):
   bf16/fp16 out: |c - ref| <= 1e-2 * |ref| + 1e-5 * sqrt(K) * sum_k |a||b| + 1e-3 (half ulp near 0)
 
 Every kernel family the router can pick is covered: the fp32 MFMA kernel, the 16-bit direct-load
-kernel (bf16, half output and fp32 output), the small-K persistent kernel (fp16, K = 128, >= 1024
+kernel (bf16, half output and fp32 output; 128x128 and 256x256 tiles), the small-K persistent kernel (fp16, K = 128, >= 1024
 tiles) and both GEMV kernels (matrix-core: bf16 at M = 1 and 8; dot-product: fp32, and bf16
 narrower than 64 columns), with per-column, full and batch-broadcast bias.
 """
@@ -128,10 +128,19 @@ def test_direct_load_column_bias_vector_rows(dt_in, dt_out, act, bias_kind):
 @pytest.mark.parametrize("act", [tv.ACT_SILU, tv.ACT_TANH])
 @pytest.mark.parametrize("bias_kind", ["col", "full"])
 def test_stream_k_fused(act, bias_kind):
-    """The fused epilogue on the stream-K schedules: bf16 with 6 tiles of 256x256 (direct-load
+    """The fused epilogue on the stream-K schedules: bf16 with 18 tiles of 128x128 (direct-load
     kernel) and fp32 with 12 tiles of 128x128, both over K long enough to split every tile."""
     run_case(tv.BFLOAT16, tv.BFLOAT16, 0, 300, 4096, 700, bias_kind, act, seed=31)
     run_case(tv.FLOAT32, tv.FLOAT32, 0, 300, 2048, 500, bias_kind, act, seed=32)
+
+
+@pytest.mark.parametrize("act", [tv.ACT_RELU, tv.ACT_SILU])
+@pytest.mark.parametrize("N,bt", [(4104, False), (4100, True)], ids=["N4104", "N4100-Bt"])
+def test_direct_load_256_tiles_fused(act, N, bt):
+    """More 128x128 tiles than fit one round of resident workgroups (561 here): the 16-bit GEMM runs
+    153 tiles of 256x256, with the fused column bias and activation; rows of C in whole 16-byte
+    chunks (N = 4104), or not (N = 4100, B a K-contiguous view so that it still loads directly)."""
+    run_case(tv.BFLOAT16, tv.BFLOAT16, 0, 2100, 256, N, "col", act, bt=bt, seed=41)
 
 
 @pytest.mark.parametrize("act", [tv.ACT_RELU, tv.ACT_SILU])

@@ -269,9 +269,9 @@ def test_small_k_persistent_exact(hip, dt, K, bt):
 @pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, INT8])
 @pytest.mark.parametrize("batch,M,K,N", [(0, 512, 8192, 1024), (0, 300, 8192, 700), (2, 200, 8192, 520), (0, 1000, 8208, 1000)])
 def test_direct_load_stream_k_bit_exact(hip, dt, batch, M, K, N):
-    """16-bit and int8 GEMMs with few, long 256x256 tiles (8, 6, 6 and 16 tiles; K = 8192 and a
-    ragged 8208) run the direct-load kernel's stream-K schedule: tiles summed in segments by
-    several workgroups.  Integer-valued inputs: exact fp32 / int32 sums in any order, so the half
+    """16-bit and int8 GEMMs with few, long tiles (16-bit: 32, 18, 20 and 64 tiles of 128x128;
+    int8: 8, 6, 6 and 16 of 256x256; K = 8192 and a ragged 8208) run the direct-load kernel's
+    stream-K schedule: tiles summed in segments by several workgroups.  Integer-valued inputs: exact fp32 / int32 sums in any order, so the half
     outputs are the exact sums rounded once, int8 the low byte, and everything equals the plain
     kernel's result (tv_hip_gemm_noalloc takes no workspace, hence no stream-K)."""
     lead = (batch,) if batch else ()
@@ -297,6 +297,36 @@ def test_direct_load_stream_k_bit_exact(hip, dt, batch, M, K, N):
     tv.check(tv.lib().tv_hip_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(to_storage(plain), c)
+
+
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16])
+@pytest.mark.parametrize("batch,M,K,N,a_t,b_t", [
+    (0, 2048, 1000, 4096, False, False),  # 512 tiles of 128x128: two per CU, the most on that size
+    (0, 130, 8208, 8000, False, False),   # 126 tiles of 128x128 over 129 k-tiles: split (stream-K)
+    (5, 1000, 304, 1096, True, True),     # 360 tiles of 128x128 over a batch, both operands transposed
+    (0, 2100, 520, 4104, False, False),   # 561 tiles of 128x128: runs 153 tiles of 256x256 instead
+    (0, 2104, 520, 4104, True, False),
+    (0, 2100, 520, 4104, False, True)],
+    ids=["t128-512", "t128-split", "t128-batch-AtBt", "t256-153", "t256-At", "t256-Bt"])
+def test_direct_load_tile_size_exact(hip, dt, batch, M, K, N, a_t, b_t):
+    """16-bit GEMMs on the direct-load kernels run 128x128 tiles while those fit one round of
+    resident workgroups (two per CU: at most 512 tiles on 256 CUs) and 256x256 tiles above that.
+    Shapes either side of the switch, ragged in M, N and K, with transposed views (every pitch a
+    whole number of 16-byte chunks, so the direct-load kernels take them).  Integer-valued inputs
+    in [-2, 2]: exact fp32 sums in any order, each rounded once; a second call gives the same bits."""
+    lead = (batch,) if batch else ()
+    x = ints(22, lead + (M, K), -2, 2)
+    y = ints(23, lead + (K, N), -2, 2)
+
+    def dev(v, transposed):
+        if transposed:
+            return to_torch(half_bits(np.ascontiguousarray(np.swapaxes(v, -1, -2)), dt), dt).transpose(-1, -2)
+        return to_torch(half_bits(v, dt), dt)
+
+    ta, tb = dev(x, a_t), dev(y, b_t)
+    c = to_storage(hip.gemm(ta, tb))
+    np.testing.assert_array_equal(c, half_bits(np.matmul(x, y), dt))
+    np.testing.assert_array_equal(to_storage(hip.gemm(ta, tb)), c)
 
 
 @pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16])
