@@ -94,7 +94,7 @@ KERNEL = {
     "c2": "gemm_dma_kernel<GemmCfg<signed char, 256, 256, 2, 4, 0, 1>, false>",
     "c3": "gemm_dma_chain_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>> (chained tiles)",
     "c3_fused": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, true>",
-    "c4": "gemm_smallk_kernel<GemmCfg<_Float16, 256, 256, 2, 4, 0, 0>>",
+    "c4": "gemm_smallk_pipe_kernel<GemmCfg<_Float16, 128, 128, 2, 4, 0, 0>, _Float16> (row-synchronous groups)",
     "c5m1": "gemv_mfma_kernel<__bf16, 4, 2>",
     "c5m8": "gemv_mfma_kernel<__bf16, 4, 2>",
 }
@@ -105,7 +105,7 @@ TRACE_KERNEL = {
     "c2": r"gemm_dma_kernel.*(GemmCfg<signed char, 256, 256|GemmCfgIaLi256ELi256E)",
     "c3": r"gemm_dma_chain_kernel.*(GemmCfg<__bf16|GemmCfgIDF16b)",
     "c3_fused": r"gemm_dma_kernel.*(GemmCfg<__bf16|GemmCfgIDF16b).*(true|Lb1E)",
-    "c4": r"gemm_smallk_kernel.*(GemmCfg<_Float16|GemmCfgIDF16_)",
+    "c4": r"gemm_smallk_pipe_kernel.*(GemmCfg<_Float16|GemmCfgIDF16_)",
     "c5m1": r"gemv_mfma_kernel.*(__bf16|DF16b)",
     "c5m8": r"gemv_mfma_kernel.*(__bf16|DF16b)",
     "cast_c3a": r"cast_kernel", "random_c3a": r"random_kernel", "fill_c3a": r"fill_kernel",

@@ -804,6 +804,209 @@ void gemm_smallk_kernel(GemmDesc d, int tiles_m, int tiles_n) {
     wait_vmcnt<0>();
 }
 
+// Small K, 16-bit: each tile's stores spread over the next tile's MFMAs, and the tiles ordered so
+// that the workgroups running at any moment write whole runs of rows of C.  At small K the output
+// stores are the work (c4: 268 MB of C against 34 MB of operands); what they cost depends on their
+// order: with each workgroup taking a contiguous run of (batch, m, n) tiles, the 256 workgroups
+// write 256-byte pieces of 128 rows each, 4 KB apart and scattered over C, and c4's stores run at
+// 3.8 TB/s; with the 16 column tiles of a row block taken by 16 workgroups at the same time, the
+// same stores run at about 5.5 TB/s (c4 72 against 49 us with the operand loads dropped).
+//  * Workgroups form groups of P = ceil(tiles_n / 2); workgroup p of a group stores column tiles p
+//    and p + P of each row block (batch, m) in the group's contiguous range, one after the other,
+//    so one load of A serves two tiles (A's loads compete with the stores for the CU's memory
+//    path: c4 loading A for every tile ran 9 % slower).  The group writes the left half of the
+//    row block's rows, then the right half.
+//  * LDS: A double-buffered (2 x 32 KB, loaded one row block ahead), one B per column tile
+//    (2 x 32 KB, reloaded at a new batch in the iteration after its last use), and the output
+//    tile (128 rows of 256 bytes, the 16-byte chunks of row r XOR-ed with r % 16, so neither the
+//    fragment writes nor the row reads conflict): 160 KB.
+//  * The output of a tile waits in LDS; the next iteration issues one store per wave after each
+//    k-group of 8 MFMAs.  That iteration's loads were issued before those stores, so the wait at
+//    its end leaves the 4 stores in flight (vmcnt retires in issue order).
+//  * Each wave stores 16 whole rows of the tile, 4 rows per instruction, with the streaming
+//    policy (nt sc1): whole 128-byte lines.  Stores outside C (the first iteration's, which has no
+//    previous tile, and column tile p + P where it is past N) get an out-of-range offset, so every
+//    wave issues the same count.
+template <class C, typename TC>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS), amdgpu_waves_per_eu(2, 2)))
+void gemm_smallk_pipe_kernel(GemmDesc d, int tiles_m, int tiles_n, int ngroups) {
+    using T = typename C::T;
+    using Op = Mfma<T>;
+    using Acc = typename Op::Acc;
+    constexpr int ES = C::ES;
+    static_assert(ES == 2 && sizeof(TC) == 2 && C::BM == 128 && C::BN == 128 && C::THREADS == 512,
+                  "16-bit inputs and output, 128x128 tiles, 8 waves");
+    using LA = DmaOperand<C::AMODE, C::BM, C::THREADS, ES>;
+    using LB = DmaOperand<C::BMODE, C::BN, C::THREADS, ES>;
+    constexpr int NWAVES = C::THREADS / 64;
+    constexpr int OROW = C::BN * ES;               // bytes of one output row (16 chunks)
+    constexpr int RPW = C::BM / NWAVES;            // output rows each wave stores
+    constexpr int CPR = OROW / 16;                 // 16-byte chunks per output row
+    constexpr int NST = RPW * CPR / 64;            // store instructions per wave and tile
+    constexpr int RPS = 64 / CPR;                  // rows per store instruction
+    static_assert(NST == 4 && CPR == 16 && C::FM * C::FN == 8, "one store after each k-group of 8 MFMAs");
+
+    __shared__ __attribute__((aligned(1024))) char SA[2][2 * LA::BYTES];
+    __shared__ __attribute__((aligned(1024))) char SB[2][2 * LB::BYTES]; // SB[s]: B of column tile s
+    __shared__ __attribute__((aligned(1024))) char SO[C::BM * OROW];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+
+    LA la;
+    LB lb;
+    la.s_r = d.sa_m; la.s_k = d.sa_k; la.K = d.K;
+    lb.s_r = d.sb_n; lb.s_k = d.sb_k; lb.K = d.K;
+    la.frag_init(lane, wm * C::WM);
+    lb.frag_init(lane, wn * C::WN);
+
+    // The grid is ngroups * P workgroups; ids are remapped so that neighbouring ids (one group,
+    // sharing A) run on one XCD.
+    const int P = (tiles_n + 1) >> 1;
+    const int G = gridDim.x;
+    int w = blockIdx.x;
+    if ((G & 7) == 0) w = (w & 7) * (G >> 3) + (w >> 3);
+    const int grp = w / P;
+    const int p = w - grp * P;
+    const int n0_0 = p * C::BN, n0_1 = (p + P) * C::BN; // the second may lie past N: no reads, no stores
+    const int R = tiles_m * d.batch; // row blocks (batch, m)
+    const int r_begin = (int)((int64_t)grp * R / ngroups);
+    const int r_end = (int)((int64_t)(grp + 1) * R / ngroups);
+    if (r_begin >= r_end) return; // uniform
+
+    auto load_a = [&](int r, char* dst) {
+        const int b = r / tiles_m, m0 = (r - b * tiles_m) * C::BM;
+        la.base = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + (int64_t)m0 * d.sa_m) * ES;
+        la.rows_valid = d.M - m0;
+        la.init(wave, lane);
+        la.issue(dst, wave, 0);
+        la.issue(dst + LA::BYTES, wave, C::BK); // zeros when K fits in one k-tile
+    };
+    auto load_b = [&](int b, int n0, char* dst) {
+        lb.base = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)n0 * d.sb_n) * ES;
+        lb.rows_valid = d.N - n0; // <= 0: every lane out of range, zeros
+        lb.init(wave, lane);
+        lb.issue(dst, wave, 0);
+        lb.issue(dst + LB::BYTES, wave, C::BK);
+    };
+
+    const int64_t cbytes = ((int64_t)(d.M - 1) * d.sc_m + d.N) * ES;
+    // This lane's output chunks: rows wave*RPW + s*RPS + lane/CPR, chunk lane%CPR.
+    const int srow = wave * RPW + lane / CPR;
+    const int schunk = lane % CPR;
+    // Reads this lane's rows of the staged output (row block pr, column tile origin pn0) from LDS and
+    // makes their global offsets.
+    auto stage_out = [&](int pr, int pn0, u32x4 (&v)[NST], unsigned (&off)[NST]) {
+        const int pb = pr < 0 ? 0 : pr / tiles_m;
+        const int pm0 = pr < 0 ? 0 : (pr - pb * tiles_m) * C::BM;
+#pragma unroll
+        for (int s = 0; s < NST; ++s) {
+            const int lr = srow + s * RPS;
+            v[s] = *reinterpret_cast<const u32x4*>(SO + lr * OROW + ((schunk ^ (lr & 15)) << 4));
+            const int row = pm0 + lr;
+            const int col = pn0 + schunk * (16 / ES);
+            off[s] = pr >= 0 && row < d.M && col < d.N ? (unsigned)(((int64_t)row * d.sc_m + col) * ES) : kOOB;
+        }
+        return make_rsrc(static_cast<const char*>(d.C) + (int64_t)pb * d.sc_b * ES, cbytes);
+    };
+
+    {
+        const int b = r_begin / tiles_m;
+        load_a(r_begin, SA[0]);
+        load_b(b, n0_0, SB[0]);
+        load_b(b, n0_1, SB[1]);
+    }
+    wait_vmcnt<0>();
+    dma_barrier();
+
+    int pr = -1, pn0 = 0; // the tile whose output is in SO (pr < 0: none yet)
+    int ca = 0;
+    for (int r = r_begin; r < r_end; ++r) {
+        const int b = r / tiles_m;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            // Operands of later tiles into buffers that no later MFMA of this row block reads
+            // (uniform conditions): A of the next row block; at a new batch, B of column tile 1
+            // (last read by the previous row block) and then B of column tile 0 for the next row
+            // block (last read by this row block's first tile).
+            if (s == 0) {
+                if (r + 1 < r_end) load_a(r + 1, SA[ca ^ 1]);
+                if (r > r_begin && b != (r - 1) / tiles_m) load_b(b, n0_1, SB[1]);
+            } else if (r + 1 < r_end && (r + 1) / tiles_m != b) {
+                load_b((r + 1) / tiles_m, n0_0, SB[0]);
+            }
+            u32x4 sv[NST];
+            unsigned soff[NST];
+            const __amdgpu_buffer_rsrc_t cr = stage_out(pr, pn0, sv, soff);
+
+            Acc acc[C::FM][C::FN];
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+            const char* sa = SA[ca];
+            const char* sb = SB[s];
+            u32x4 fa[2][C::FM], fb[2][C::FN];
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) fb[0][j] = lb.frag(sb, 0, j);
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i) fa[0][i] = la.frag(sa, 0, i);
+            // k-group g = 2 * k-tile + group inside the k-tile; the next group's fragments are
+            // read while this group's MFMAs run, and one store goes out after each group.
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int x = g & 1;
+                if (g < 3) {
+                    const int kt = (g + 1) >> 1, kg = (g + 1) & 1;
+#pragma unroll
+                    for (int j = 0; j < C::FN; ++j) fb[x ^ 1][j] = lb.frag(sb + kt * LB::BYTES, kg, j);
+#pragma unroll
+                    for (int i = 0; i < C::FM; ++i) fa[x ^ 1][i] = la.frag(sa + kt * LA::BYTES, kg, i);
+                }
+#pragma unroll
+                for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < C::FN; ++j) Op::run(fb[x][j], fa[x][i], acc[i][j]);
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, sv[g]), cr, (int)soff[g], 0, 18);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            dma_barrier(); // every wave is done with these operands and with the staged output
+
+            // This tile's output into SO: acc[i][j][q] is tile row wm*WM + 16i + lane%16, column
+            // wn*WN + 16j + 4*(lane/16) + q; 8 bytes at byte 2*column of the row, chunk-swizzled.
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j) {
+                    const int row = wm * C::WM + 16 * i + (lane & 15);
+                    const int cbyte = (wn * C::WN + 16 * j + 4 * (lane >> 4)) * ES;
+                    typedef TC v4 __attribute__((__vector_size__(4 * sizeof(TC))));
+                    const v4 h = {cvt_out<TC>(acc[i][j][0]), cvt_out<TC>(acc[i][j][1]), cvt_out<TC>(acc[i][j][2]),
+                                  cvt_out<TC>(acc[i][j][3])};
+                    *reinterpret_cast<uint2*>(SO + row * OROW + (((cbyte >> 4) ^ (row & 15)) << 4) + (cbyte & 15)) =
+                        __builtin_bit_cast(uint2, h);
+                }
+            wait_vmcnt<NST>(); // this iteration's loads (issued before its stores)
+            dma_barrier();     // ... and this tile's staged output are visible to every wave
+            pr = r;
+            pn0 = s ? n0_1 : n0_0;
+        }
+        ca ^= 1;
+    }
+    {
+        u32x4 sv[NST];
+        unsigned soff[NST];
+        const __amdgpu_buffer_rsrc_t cr = stage_out(pr, pn0, sv, soff);
+#pragma unroll
+        for (int s = 0; s < NST; ++s)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, sv[s]), cr, (int)soff[s], 0, 18);
+    }
+    wait_vmcnt<0>();
+}
+
 // Persistent direct-load GEMM for launches of several tiles per CU (one resident workgroup per
 // CU).  The k-loop runs on from one tile into the next: the last two k-steps of a tile load
 // k-tiles 0 and 1 of the workgroup's next tile, so when a tile's output is stored the next tile's
@@ -1056,18 +1259,6 @@ static int run_smallk_cfg(const GemmDesc& d, hipStream_t stream) {
     return hipGetLastError();
 }
 
-static bool smallk_ok(const GemmDesc& d, int es, int bm_rows, int bn_rows) {
-    const size_t csz = dtype_size(d.dtype_c);
-    if (d.K > 2 * (128 / es) || csz != (size_t)es) return false;
-    if (d.N % (16 / (int64_t)csz) != 0) return false;
-    if (((int64_t)(d.M - 1) * d.sc_m + d.N) * (int64_t)csz >= ((int64_t)1 << 30)) return false;
-    if (!(d.sc_n == 1 && (reinterpret_cast<uintptr_t>(d.C) % 16) == 0 && d.sc_m % (16 / (int64_t)csz) == 0 &&
-          (d.batch <= 1 || d.sc_b % (16 / (int64_t)csz) == 0)))
-        return false;
-    const int64_t tiles = (int64_t)((d.M + bm_rows - 1) / bm_rows) * ((d.N + bn_rows - 1) / bn_rows) * d.batch;
-    return tiles >= 1024;
-}
-
 // Compute units of the current device (cached per device; 256 if the runtime cannot tell).
 static int device_cus() {
     static int cached[64] = {};
@@ -1080,6 +1271,43 @@ static int device_cus() {
     return cached[dev];
 }
 
+// The 16-bit small-K path: 128x128 tiles, groups of ceil(tiles_n / 2) persistent workgroups (one
+// per CU: its LDS admits one) that store runs of whole rows of C together
+// (gemm_smallk_pipe_kernel).  Returns 1 if the groups do not fill the CUs well (more than an
+// eighth of them would idle).
+template <class C>
+static int run_smallk_pipe_cfg(const GemmDesc& d, hipStream_t stream) {
+    const int64_t tiles_m = (d.M + C::BM - 1) / C::BM;
+    const int64_t tiles_n = (d.N + C::BN - 1) / C::BN;
+    const int64_t rows = tiles_m * d.batch;
+    if (rows * tiles_n > 0x7FFFFFFF) return TV_E_SHAPE;
+    const int cus = device_cus();
+    const int64_t P = (tiles_n + 1) / 2;
+    if (P > cus || (cus % P) * 8 > cus) return 1;
+    const int64_t ngroups = cus / P < rows ? cus / P : rows;
+    const int grid = (int)(ngroups * P);
+    if (d.dtype_c == TV_BFLOAT16)
+        hipLaunchKernelGGL((gemm_smallk_pipe_kernel<C, __bf16>), dim3((unsigned)grid), dim3(C::THREADS), 0, stream, d, (int)tiles_m,
+                           (int)tiles_n, (int)ngroups);
+    else
+        hipLaunchKernelGGL((gemm_smallk_pipe_kernel<C, _Float16>), dim3((unsigned)grid), dim3(C::THREADS), 0, stream, d, (int)tiles_m,
+                           (int)tiles_n, (int)ngroups);
+    return hipGetLastError();
+}
+
+static bool smallk_ok(const GemmDesc& d, int es, int bm_rows, int bn_rows) {
+    const size_t csz = dtype_size(d.dtype_c);
+    if (d.K > 2 * (128 / es) || csz != (size_t)es) return false;
+    if (d.N % (16 / (int64_t)csz) != 0) return false;
+    if (((int64_t)(d.M - 1) * d.sc_m + d.N) * (int64_t)csz >= ((int64_t)1 << 30)) return false;
+    if (!(d.sc_n == 1 && (reinterpret_cast<uintptr_t>(d.C) % 16) == 0 && d.sc_m % (16 / (int64_t)csz) == 0 &&
+          (d.batch <= 1 || d.sc_b % (16 / (int64_t)csz) == 0)))
+        return false;
+    const int64_t tiles = (int64_t)((d.M + bm_rows - 1) / bm_rows) * ((d.N + bn_rows - 1) / bn_rows) * d.batch;
+    return tiles >= 1024;
+}
+
+
 // 16-bit / int8 inputs: direct-to-LDS kernel for the vector layouts, gemm_mfma_kernel otherwise.
 template <typename T, int BM, int BN, int WMW, int WNW>
 static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m, bool may_alloc) {
@@ -1089,8 +1317,14 @@ static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m, boo
     // The small-K kernel has no fused epilogue (its staging area holds the output type only).
     const bool epi = d.bias != nullptr || d.act != TV_ACT_NONE;
     if (!epi && am != LOAD_GENERIC && bm != LOAD_GENERIC && smallk_ok(d, es, BM, BN)) {
-#define TV_CASE(A_, B_) \
-    if (am == A_ && bm == B_) return run_smallk_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream);
+#define TV_CASE(A_, B_)                                                                                      \
+    if (am == A_ && bm == B_) {                                                                              \
+        if constexpr (sizeof(T) == 2) {                                                                      \
+            const int rc = run_smallk_pipe_cfg<GemmCfg<T, 128, 128, 2, 4, A_, B_>>(d, stream);               \
+            if (rc != 1) return rc;                                                                          \
+        }                                                                                                    \
+        return run_smallk_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream);                              \
+    }
         TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)
         TV_CASE(LOAD_KCONTIG, LOAD_KCONTIG)
         TV_CASE(LOAD_MNCONTIG, LOAD_MNCONTIG)

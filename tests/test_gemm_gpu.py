@@ -266,6 +266,24 @@ def test_small_k_persistent_exact(hip, dt, K, bt):
     np.testing.assert_array_equal(c, want)
 
 
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16])
+@pytest.mark.parametrize("batch,M,K,N,bt", [(16, 1100, 40, 3832, False), (4, 2048, 32, 9216, True)],
+                         ids=["groups-of-30", "72-columns-fallback"])
+def test_small_k_row_groups_exact(hip, dt, batch, M, K, N, bt):
+    """16-bit small-K GEMMs run 128x128 tiles in groups of as many workgroups as C has column tiles,
+    each group walking its own run of row blocks: 30 column tiles make 8 groups of 240 workgroups
+    (ragged M, N and K, one B per batch, so B reloads inside a group's run).  With 72 column tiles
+    a third of the CUs would idle, so that shape runs the 256x256 small-K kernel instead.
+    Integer-valued inputs in [-2, 2]: exact sums, each rounded once."""
+    x = ints(24, (batch, M, K), -2, 2)
+    y = ints(25, (batch, K, N), -2, 2)
+    ta = to_torch(half_bits(x, dt), dt)
+    tb = (to_torch(half_bits(np.ascontiguousarray(np.swapaxes(y, 1, 2)), dt), dt).permute(0, 2, 1) if bt
+          else to_torch(half_bits(y, dt), dt))
+    c = to_storage(hip.gemm(ta, tb))
+    np.testing.assert_array_equal(c, half_bits(np.matmul(x, y), dt))
+
+
 @pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, INT8])
 @pytest.mark.parametrize("batch,M,K,N", [(0, 512, 8192, 1024), (0, 300, 8192, 700), (2, 200, 8192, 520), (0, 1000, 8208, 1000)])
 def test_direct_load_stream_k_bit_exact(hip, dt, batch, M, K, N):
