@@ -1158,15 +1158,17 @@ static int run_dma_chain(const GemmDesc& d, hipStream_t stream, int group_m, int
     return hipGetLastError();
 }
 
-// Stream-K launch of the direct-load kernel for few, long tiles: at most a quarter as many tiles as
-// resident workgroups and K of at least 64 k-tiles.  A split tile moves its fp32 partial sums
+// Stream-K launch of the direct-load kernel for few, long tiles: at most a quarter as many 256x256
+// tiles (half as many 128x128 tiles) as resident workgroups, and K of at least 64 k-tiles.  A split tile moves its fp32 partial sums
 // through the slots once per segment, which costs more than the balance gains once the tiles are
 // many.  Measured (settled clocks, same box, against one workgroup per tile) on int8 256x256 tiles
 // (one resident per CU): [512,8192]@[8192,8192] 52.0 against 75.5 us; and on bf16 256x256 tiles
 // before 16-bit GEMMs this small moved to 128x128 tiles: [512,8192]@[8192,8192] 88.9 against
 // 146.7 us, but 192 tiles (M = 3000, K = 4096) 121.5 against 83.0 us.  bf16 [128,8192]@[8192,8192]
 // (64 tiles of 128x128, two resident per CU) runs 43.5 us split.  c2 (256 tiles) and c3 (2048)
-// keep one workgroup per tile.  Returns 1 if it did not launch.
+// keep one workgroup per tile.  128x128 tiles split at up to half the resident workgroups: bf16
+// [512,8192]@[8192,8192] (256 tiles on 512 slots) 74.2 against 79.2 us, [1024,8192]@[8192,4096]
+// 74.5 against 80.1, [1024,4096]@[4096,4096] 43.0 against 45.1.  Returns 1 if it did not launch.
 template <class C, bool FUSED>
 static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int tiles_m, int tiles_n, int64_t ntiles, int c_vec) {
     const int nk = (d.K + C::BK - 1) / C::BK;
@@ -1183,7 +1185,7 @@ static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int ti
         grid[dev] = per_cu * cus;
     }
     int G = grid[dev];
-    if (ntiles * 4 > G) return 1;
+    if (ntiles * (C::BM == 128 ? 2 : 4) > G) return 1;
     const int64_t iters = ntiles * nk;
     if (iters / 8 < G) G = (int)(iters / 8);
     if (G < 1) return 1;
