@@ -56,7 +56,6 @@ static unsigned ew_blocks(int64_t n) {
     return (unsigned)(b < 1 ? 1 : b);
 }
 
-static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // ---- typecast ----------------------------------------------------------------------------------
 

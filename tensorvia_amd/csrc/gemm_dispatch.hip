@@ -7,7 +7,63 @@ int launch_gemm_mfma_bf16(const GemmDesc& d, hipStream_t stream, bool may_alloc)
 int launch_gemm_mfma_f16(const GemmDesc& d, hipStream_t stream, bool may_alloc);
 int launch_gemm_mfma_i8(const GemmDesc& d, hipStream_t stream, bool may_alloc);
 
-int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream, bool may_alloc) {
+// An operand contiguous along one dimension whose rows are not whole 16-byte chunks (row length,
+// pitch, batch stride or base address) would be read by the element-gather loader, one load per
+// element: bf16 [2048,4096] @ [4096,4100] took 1.18 ms that way, against about 0.1 ms on the
+// vector loaders.  With a workspace, such an operand is copied once into rows of whole chunks, zero
+// past its valid extent (pad_a / pad_b tell the load-mode choice that the tail may be read), and
+// the GEMM runs on the copy.  Small GEMMs keep the gather (the copy would be the larger cost).
+static int pad_operand(GemmDesc& d, bool is_a, hipStream_t stream) {
+    const int es = (int)dtype_size(is_a ? d.dtype_a : d.dtype_b);
+    if (es != 1 && es != 2 && es != 4) return 0;
+    const int64_t vec = 16 / es;
+    const void* p = is_a ? d.A : d.B;
+    const int64_t R = is_a ? d.M : d.N, K = d.K;
+    const int64_t s_r = is_a ? d.sa_m : d.sb_n, s_k = is_a ? d.sa_k : d.sb_k, s_b = is_a ? d.sa_b : d.sb_b;
+    if (pick_mode(p, R, K, s_r, s_k, s_b, d.batch, es, 256, false) != LOAD_GENERIC) return 0;
+    int64_t L, rows, s_row;
+    if (s_k == 1) { // rows (m / n) of L = K contiguous elements
+        L = K;
+        rows = R;
+        s_row = s_r;
+    } else if (s_r == 1) { // k rows of L = M / N contiguous elements
+        L = R;
+        rows = K;
+        s_row = s_k;
+    } else {
+        return 0; // no contiguous dimension: the gather stays
+    }
+    if (L <= 0 || rows <= 0) return 0;
+    const int64_t P = (L + vec - 1) / vec * vec;
+    const int64_t nb = d.batch > 1 && s_b != 0 ? d.batch : 1;
+    void* ws = nullptr;
+    if (gemm_pad_workspace(stream, (size_t)(nb * rows * P * es), is_a ? 0 : 1, &ws) != 0) return 0; // no room: gather
+    const int rc = launch_pad_rows(p, ws, es, nb, rows, s_row, s_b, L, P, stream);
+    if (rc) return rc;
+    if (is_a) {
+        d.A = ws;
+        (s_k == 1 ? d.sa_m : d.sa_k) = P;
+        d.sa_b = nb > 1 ? rows * P : 0;
+        d.pad_a = 1;
+    } else {
+        d.B = ws;
+        (s_k == 1 ? d.sb_n : d.sb_k) = P;
+        d.sb_b = nb > 1 ? rows * P : 0;
+        d.pad_b = 1;
+    }
+    return 0;
+}
+
+// GEMMs of at least this many multiply-adds copy misaligned operands (pad_operand).
+constexpr int64_t kPadMinMacs = (int64_t)1 << 24;
+
+int launch_gemm_mfma(const GemmDesc& d0, hipStream_t stream, bool may_alloc) {
+    GemmDesc d = d0;
+    if (may_alloc && (int64_t)d.M * d.N * d.K * (d.batch > 1 ? d.batch : 1) >= kPadMinMacs) {
+        int rc = pad_operand(d, true, stream);
+        if (rc == 0) rc = pad_operand(d, false, stream);
+        if (rc) return rc;
+    }
     switch (d.dtype_a) {
         case TV_FLOAT32: return launch_gemm_mfma_f32(d, stream, may_alloc);
         case TV_BFLOAT16: return launch_gemm_mfma_bf16(d, stream, may_alloc);

@@ -1314,8 +1314,8 @@ static bool smallk_ok(const GemmDesc& d, int es, int bm_rows, int bn_rows) {
 template <typename T, int BM, int BN, int WMW, int WNW>
 static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m, bool may_alloc) {
     const int es = (int)sizeof(T);
-    const int am = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, BM);
-    const int bm = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, BN);
+    const int am = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, BM, d.pad_a);
+    const int bm = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, BN, d.pad_b);
     // The small-K kernel has no fused epilogue (its staging area holds the output type only).
     const bool epi = d.bias != nullptr || d.act != TV_ACT_NONE;
     if (!epi && am != LOAD_GENERIC && bm != LOAD_GENERIC && smallk_ok(d, es, BM, BN)) {

@@ -845,27 +845,6 @@ void gemm_mfma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int 
 
 // ---------------------------------------------------------------------------------------------
 // Host side: pick the operand load modes and the tile configuration.
-static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
-
-// Mode for one operand.  `rows` extent R, strides s_r (along rows), s_k (along k), s_b (batch).
-// The vector modes also need every per-lane offset inside one k-tile panel to fit in 31 bits.
-static int pick_mode(const void* p, int64_t R, int64_t K, int64_t s_r, int64_t s_k, int64_t s_b, int64_t batch,
-                     int es, int rows_tile) {
-    const int64_t vec = 16 / es;
-    const int64_t bk = 128 / es;
-    const bool ok_ptr = aligned16(p);
-    const bool ok_b = batch <= 1 || s_b % vec == 0;
-    const int64_t lim = (int64_t)1 << 30;
-    // Tails are masked by the buffer range check, which needs rows (k rows) that do not overlap.
-    if (s_k == 1 && ok_ptr && ok_b && K % vec == 0 && (R <= 1 || (s_r % vec == 0 && s_r >= K)) &&
-        ((int64_t)rows_tile * s_r + bk) * es < lim)
-        return LOAD_KCONTIG;
-    if (s_r == 1 && ok_ptr && ok_b && R % vec == 0 && (K <= 1 || (s_k % vec == 0 && s_k >= R)) &&
-        (bk * s_k + rows_tile) * es < lim)
-        return LOAD_MNCONTIG;
-    return LOAD_GENERIC;
-}
-
 // Workgroups of the stream-K kernel resident at once on the current device (occupancy API x CUs),
 // cached per device; 0 if the runtime cannot tell.
 template <class C>
@@ -955,8 +934,8 @@ static int run_cfg(const GemmDesc& d, hipStream_t stream, int group_m, bool may_
 template <typename T, int BM, int BN, int WMW, int WNW>
 static int run_modes(const GemmDesc& d, hipStream_t stream, int group_m, bool may_alloc = true) {
     const int es = (int)sizeof(T);
-    const int am = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, BM);
-    const int bm = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, BN);
+    const int am = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, BM, d.pad_a);
+    const int bm = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, BN, d.pad_b);
 #define TV_CASE(A_, B_) \
     if (am == A_ && bm == B_) return run_cfg<GemmCfg<T, BM, BN, WMW, WNW, A_, B_>>(d, stream, group_m, may_alloc);
     TV_CASE(LOAD_KCONTIG, LOAD_MNCONTIG)
@@ -965,8 +944,8 @@ static int run_modes(const GemmDesc& d, hipStream_t stream, int group_m, bool ma
     TV_CASE(LOAD_MNCONTIG, LOAD_KCONTIG)
 #undef TV_CASE
     // Gather paths: re-pick the modes for the small tile's row count.
-    const int am2 = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, 128);
-    const int bm2 = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, 128);
+    const int am2 = pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, es, 128, d.pad_a);
+    const int bm2 = pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, es, 128, d.pad_b);
 #define TV_CASE(A_, B_) \
     if (am2 == A_ && bm2 == B_) return run_cfg<GemmCfg<T, 128, 128, 2, 2, A_, B_>>(d, stream, group_m, may_alloc);
     TV_CASE(LOAD_KCONTIG, LOAD_GENERIC)

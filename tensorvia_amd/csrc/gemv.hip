@@ -531,7 +531,8 @@ static std::mutex g_ws_mu;
 static std::map<std::tuple<int, hipStream_t, int>, GemvWorkspace> g_ws;
 
 // kind 1: the GEMV's split-K arrival counters (every launch leaves them at zero); kind 2: its strip
-// partial slots; kinds 3 and 4: the same for the stream-K GEMM schedule (gemm_sk_workspace).
+// partial slots; kinds 3 and 4: the same for the stream-K GEMM schedule (gemm_sk_workspace); kinds
+// 5 and 6: the zero-padded copies of GEMM operands A and B (gemm_pad_workspace).
 static int get_workspace(hipStream_t stream, size_t need, void** out, int kind) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -592,6 +593,11 @@ int gemm_sk_workspace(hipStream_t stream, size_t cnt_ints, size_t slot_bytes, in
     *cnt = static_cast<int*>(c);
     *slots = static_cast<char*>(p);
     return 0;
+}
+
+// Buffer of the zero-padded copy of GEMM operand A (workspace kind 5) or B (kind 6).
+int gemm_pad_workspace(hipStream_t stream, size_t bytes, int operand, void** out) {
+    return get_workspace(stream, bytes, out, operand == 0 ? 5 : 6);
 }
 
 // Whether the vectorised GEMV serves this call.

@@ -153,6 +153,74 @@ static int launch_transpose(const RepackDesc& r, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// Zero-padded row copy of a GEMM operand (launch_gemm_mfma uses it for operands contiguous along
+// one dimension whose rows are not whole 16-byte chunks): destination row w = batch * rows + row
+// holds the source row's L elements, then zeros up to P.  One thread per 16-byte destination
+// chunk, consecutive threads on consecutive chunks (rows run on one after the other).  A chunk
+// wholly inside its row is read with the widest loads the row start's alignment allows (16, 8 or
+// 4 bytes; the same for every chunk of a row, since chunks are 16 bytes apart); a row's last,
+// partial chunk element by element.  IDX: 32-bit index arithmetic when the chunk count allows.
+template <typename E, typename IDX>
+__global__ __launch_bounds__(256) void pad_rows_kernel(const E* src, E* dst, int64_t rows, int64_t nrows, int64_t s_row,
+                                                       int64_t s_batch, int64_t L, int64_t P) {
+    constexpr int V = 16 / (int)sizeof(E);
+    struct Chunk {
+        E e[V];
+    };
+    const IDX cpr = (IDX)(P / V);
+    const IDX total = (IDX)nrows * cpr;
+    const IDX rws = (IDX)rows;
+    const IDX stride = (IDX)gridDim.x * blockDim.x;
+    for (IDX i = (IDX)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const IDX w = i / cpr, c = i - w * cpr;
+        const IDX b = rws == (IDX)nrows ? 0 : w / rws, r = w - b * rws;
+        const E* s = src + (int64_t)b * s_batch + (int64_t)r * s_row;
+        const int64_t x0 = (int64_t)c * V;
+        const char* q = reinterpret_cast<const char*>(s + x0);
+        const unsigned al = (unsigned)(reinterpret_cast<uintptr_t>(s) & 15);
+        u32x4 v;
+        if (x0 + V <= L && al == 0) {
+            v = *reinterpret_cast<const u32x4*>(q);
+        } else if (x0 + V <= L && (al & 7) == 0) {
+            const uint2 lo = reinterpret_cast<const uint2*>(q)[0], hi = reinterpret_cast<const uint2*>(q)[1];
+            v = u32x4{lo.x, lo.y, hi.x, hi.y};
+        } else if (x0 + V <= L && (al & 3) == 0) {
+            const unsigned* u = reinterpret_cast<const unsigned*>(q);
+            v = u32x4{u[0], u[1], u[2], u[3]};
+        } else {
+            Chunk t;
+#pragma unroll
+            for (int e = 0; e < V; ++e) t.e[e] = x0 + e < L ? s[x0 + e] : E(0);
+            v = __builtin_bit_cast(u32x4, t);
+        }
+        *reinterpret_cast<u32x4*>(dst + (int64_t)w * P + x0) = v;
+    }
+}
+
+int launch_pad_rows(const void* src, void* dst, int es, int64_t nb, int64_t rows, int64_t s_row, int64_t s_batch, int64_t L,
+                    int64_t P, hipStream_t stream) {
+    const int64_t nrows = nb * rows;
+    if (nrows <= 0 || L <= 0 || P < L || (P * es) % 16 != 0) return TV_E_SHAPE;
+    const int64_t chunks = nrows * (P * es / 16);
+    const unsigned grid = grid_for(chunks, 256);
+    const bool small = chunks < ((int64_t)1 << 31);
+#define TV_PAD(E)                                                                                                      \
+    if (small)                                                                                                         \
+        hipLaunchKernelGGL((pad_rows_kernel<E, uint32_t>), dim3(grid), dim3(256), 0, stream, static_cast<const E*>(src), \
+                           static_cast<E*>(dst), rows, nrows, s_row, s_batch, L, P);                                  \
+    else                                                                                                               \
+        hipLaunchKernelGGL((pad_rows_kernel<E, int64_t>), dim3(grid), dim3(256), 0, stream, static_cast<const E*>(src),  \
+                           static_cast<E*>(dst), rows, nrows, s_row, s_batch, L, P);
+    switch (es) {
+        case 1: TV_PAD(uint8_t) break;
+        case 2: TV_PAD(uint16_t) break;
+        case 4: TV_PAD(uint32_t) break;
+        default: return TV_E_DTYPE;
+    }
+#undef TV_PAD
+    return hipGetLastError();
+}
+
 int launch_repack(const tv_repack_args* a, hipStream_t stream) {
     RepackDesc r;
     r.ndim = a->ndim;

@@ -46,6 +46,9 @@ struct GemmDesc {
     int64_t sbias_b = 0, sbias_m = 0, sbias_n = 0; // element strides (0 broadcasts), non-negative
     int64_t bias_bytes = 0;                        // extent of the bias read (below 2^30)
     int32_t act = TV_ACT_NONE;
+    // 1: the operand is a copy made by launch_gemm_mfma whose rows are whole 16-byte chunks, zero
+    // past the valid extent, so a chunk that straddles the end of the valid extent may be read.
+    int32_t pad_a = 0, pad_b = 0;
 };
 
 __device__ inline bool has_epilogue(const GemmDesc& d) { return d.bias != nullptr || d.act != TV_ACT_NONE; }
@@ -128,6 +131,29 @@ enum LoadMode : int {
     LOAD_GENERIC = 2   // anything else: element gathers
 };
 
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Mode for one operand.  `rows` extent R, strides s_r (along rows), s_k (along k), s_b (batch).
+// The vector modes also need every per-lane offset inside one k-tile panel to fit in 31 bits.
+// padded: a zero-padded copy (GemmDesc::pad_a / pad_b), whose valid extent need not be whole chunks.
+inline int pick_mode(const void* p, int64_t R, int64_t K, int64_t s_r, int64_t s_k, int64_t s_b, int64_t batch, int es,
+                     int rows_tile, bool padded) {
+    const int64_t vec = 16 / es;
+    const int64_t bk = 128 / es;
+    const bool ok_ptr = aligned16(p);
+    const bool ok_b = batch <= 1 || s_b % vec == 0;
+    const int64_t lim = (int64_t)1 << 30;
+    // Tails are masked by the buffer range check, which needs rows (k rows) that do not overlap;
+    // a chunk past the valid extent would read the next row, unless that tail is zero padding.
+    if (s_k == 1 && ok_ptr && ok_b && (padded || K % vec == 0) && (R <= 1 || (s_r % vec == 0 && s_r >= K)) &&
+        ((int64_t)rows_tile * s_r + bk) * es < lim)
+        return LOAD_KCONTIG;
+    if (s_r == 1 && ok_ptr && ok_b && (padded || R % vec == 0) && (K <= 1 || (s_k % vec == 0 && s_k >= R)) &&
+        (bk * s_k + rows_tile) * es < lim)
+        return LOAD_MNCONTIG;
+    return LOAD_GENERIC;
+}
+
 // Launchers (return hipError_t, or a negative TV_E_* code).
 // may_alloc = false: no launch path that needs a grown workspace (the stream-K schedule of the fp32
 // kernel); the plain data-parallel kernels serve the call.
@@ -158,6 +184,13 @@ int launch_gemv(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed 
 int gemv_static_scratch(hipStream_t stream, GemvScratch* out);
 // GEMV with an explicit strip width (nl lanes), workgroup size and K split (tuning sweeps).
 int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices);
+// Zero-padded row copy of a GEMM operand: nb batches (source stride s_batch) of `rows` rows (source
+// stride s_row) of L contiguous elements of `es` bytes, written densely as rows of P elements (P a
+// multiple of 16 bytes), zero in [L, P).
+int launch_pad_rows(const void* src, void* dst, int es, int64_t nb, int64_t rows, int64_t s_row, int64_t s_batch,
+                    int64_t L, int64_t P, hipStream_t stream);
+// Per-(device, stream) buffer for the padded copy of operand A (operand 0) or B (operand 1).
+int gemm_pad_workspace(hipStream_t stream, size_t bytes, int operand, void** out);
 
 // Buffer loads: a lane offset at or above 2^31 is outside every buffer resource built by make_rsrc
 // (num_records <= 2^30), also after a stride multiple below 2^30 is added to it, and such a load

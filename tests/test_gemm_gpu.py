@@ -385,6 +385,44 @@ def test_direct_load_chain_transposed_views(hip, dt, a_t, b_t):
     np.testing.assert_array_equal(c, half_bits(np.matmul(x, y), dt))
 
 
+@pytest.mark.parametrize("dt", [FLOAT32, BFLOAT16, FLOAT16, INT8])
+@pytest.mark.parametrize("batch,M,K,N,a_t,b_t,bcast", [
+    (0, 1000, 700, 1030, False, False, False),  # A's rows (K) and B's k rows (N) not whole 16-byte chunks
+    (0, 1030, 1002, 700, True, True, False),    # transposed views: A M-contiguous (M = 1030), B K-contiguous (K = 1002)
+    (3, 500, 300, 998, False, False, True),     # batched A copied per batch, broadcast B copied once
+    (2, 600, 1002, 512, False, True, False)],   # per-batch K-contiguous B
+    ids=["AK-BN", "AM-BK", "batch-bcastB", "batch-BK"])
+def test_misaligned_operands_padded_exact(hip, dt, batch, M, K, N, a_t, b_t, bcast):
+    """An operand contiguous along one dimension whose rows are not whole 16-byte chunks is copied
+    once into zero-padded rows of whole chunks (large enough GEMMs, through the workspace), and the
+    GEMM runs on the vector loaders: A with K- or M-contiguous rows, B with N- or K-contiguous
+    rows, per batch or broadcast.  Integer-valued inputs: exact sums, half outputs rounded once,
+    int8 the low byte; fp32 exact."""
+    lead = (batch,) if batch else ()
+    lo, hi = (-8, 8) if dt == INT8 else (-2, 2)
+    x = ints(26, lead + (M, K), lo, hi)
+    y = ints(27, (K, N) if bcast else lead + (K, N), lo, hi)
+
+    def enc(v):
+        if dt == INT8:
+            return v.astype(np.int8)
+        return half_bits(v, dt) if dt in (BFLOAT16, FLOAT16) else v.astype(np.float32)
+
+    def dev(v, transposed):
+        if transposed:
+            return to_torch(np.ascontiguousarray(enc(np.swapaxes(v, -1, -2))), dt).transpose(-1, -2)
+        return to_torch(enc(v), dt)
+
+    c = to_storage(hip.gemm(dev(x, a_t), dev(y, b_t)))
+    exact = np.matmul(x.astype(np.float64), y.astype(np.float64))
+    if dt == INT8:
+        np.testing.assert_array_equal(c, orc.low_byte(exact.astype(np.int64)))
+    elif dt == FLOAT32:
+        np.testing.assert_array_equal(c, exact.astype(np.float32))
+    else:
+        np.testing.assert_array_equal(c, half_bits(exact.astype(np.float32), dt))
+
+
 # ---- views, offsets, batches ----------------------------------------------------------------
 
 @pytest.mark.parametrize("dt", [FLOAT32, BFLOAT16, INT8])
