@@ -45,10 +45,11 @@
  *     SIMT kernel (slow path, provided for completeness).
  *
  * Calls are asynchronous on `hip_stream` (a hipStream_t, NULL = default stream).  The caller
- * keeps A, B and C alive until the stream has executed the work.  The split-K GEMV keeps its
- * partial-sum workspace per (device, stream): calls on one stream are ordered by that stream, and
- * calls on different streams use different workspaces, so concurrent streams are safe.  Growing
- * a stream's workspace synchronises that stream once.
+ * keeps A, B and C alive until the stream has executed the work.  The split-K schedules keep their
+ * partial sums, and large GEMMs their zero-padded copies of operands whose rows are not whole
+ * 16-byte chunks, in a workspace per (device, stream): calls on one stream are ordered by that
+ * stream, and calls on different streams use different workspaces, so concurrent streams are safe.
+ * Growing a stream's workspace synchronises that stream once.
  */
 #ifndef TENSORVIA_HIP_H
 #define TENSORVIA_HIP_H
