@@ -1172,7 +1172,7 @@ static int run_dma_chain(const GemmDesc& d, hipStream_t stream, int group_m, int
 template <class C, bool FUSED>
 static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int tiles_m, int tiles_n, int64_t ntiles, int c_vec) {
     const int nk = (d.K + C::BK - 1) / C::BK;
-    if (nk < 64) return 1;
+    if (nk < (__is_same(typename C::T, int8_t) ? 16 : 64)) return 1;
     static int grid[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
@@ -1186,6 +1186,12 @@ static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int ti
     }
     int G = grid[dev];
     if (ntiles * (C::BM == 128 ? 2 : 4) > G) return 1;
+    // int8 256x256 tiles split from 16 k-tiles (K >= 2048) when they are few (at most a fifth of
+    // the resident workgroups): one such tile takes a CU about 40 us at K = 4096, so a few of them
+    // leave the chip idle (int8 [512,4096]@[4096,4096] 41.0 -> 33.3 us, [256,4096]@[4096,4096]
+    // 40.5 -> 31.6, [16,4096]@[4096,4096] 40.2 -> 31.0); 64 tiles were slower split
+    // ([2048,2048]^3 24.2 against 28.5 us).  16-bit tiles split from 64 k-tiles.
+    if (nk < 64 && ntiles * 5 > G) return 1;
     const int64_t iters = ntiles * nk;
     if (iters / 8 < G) G = (int)(iters / 8);
     // At most about four segments per tile: bf16 [256,4096]@[4096,4096] (64 tiles of 128x128)

@@ -290,9 +290,10 @@ def test_small_k_row_groups_exact(hip, dt, batch, M, K, N, bt):
 def test_direct_load_stream_k_bit_exact(hip, dt, batch, M, K, N):
     """16-bit and int8 GEMMs with few, long tiles (16-bit: 32, 18, 20, 64, 144 and 150 tiles of
     128x128, the last two in the range split only for 128x128 tiles, at most half as many tiles as
-    resident workgroups; int8: 8, 6, 6 and 16 of 256x256, while its last two shapes have too few
-    k-tiles to split; K = 8192, 4096 and the ragged 8208 and 4104) run the direct-load kernel's
-    stream-K schedule: tiles summed in segments by several workgroups.  Integer-valued inputs: exact fp32 / int32 sums in any order, so the half
+    resident workgroups; int8: 8, 6, 6, 16, 40 and 45 of 256x256, the last two split from 33 and
+    32 k-tiles, which int8 allows for at most a fifth as many tiles as resident workgroups; K =
+    8192, 4096 and the ragged 8208 and 4104) run the direct-load kernel's stream-K schedule: tiles
+    summed in segments by several workgroups.  Integer-valued inputs: exact fp32 / int32 sums in any order, so the half
     outputs are the exact sums rounded once, int8 the low byte, and everything equals the plain
     kernel's result (tv_hip_gemm_noalloc takes no workspace, hence no stream-K)."""
     lead = (batch,) if batch else ()
