@@ -96,8 +96,8 @@ struct DmaOperand {
     static constexpr int KGB = (ES == 1 ? 64 : 32) * RB;
     static constexpr int RD2 = (ES == 1 ? 8 : 4) * RB;
     static_assert(NBLK % NWAVES == 0, "load blocks must divide over the waves");
-    static_assert(MODE == LOAD_KCONTIG || (MODE == LOAD_MNCONTIG && ES <= 2 && (ROWS == 256 || (ES == 2 && ROWS == 128))),
-                  "M/N layout is laid out for 256-row int8 / 16-bit and 128-row 16-bit tiles");
+    static_assert(MODE == LOAD_KCONTIG || (MODE == LOAD_MNCONTIG && ES <= 2 && (ROWS == 256 || ROWS == 128)),
+                  "M/N layout is laid out for 256- and 128-row int8 / 16-bit tiles");
 
     const char* base; // element (row0, k = 0) of this tile, as bytes
     int64_t s_r, s_k; // element strides
@@ -107,8 +107,14 @@ struct DmaOperand {
     int kc[PER_WAVE];        // K layout: first k of the lane's chunk inside the k-tile
 
     // M/N layout swizzle: distinct 16-byte bank groups for the k rows one transpose-read pass reads.
+    // int8 with 128-byte k rows (128-row tiles): a k row covers half of the 64 banks, the row's
+    // parity picks the half, so the 16 rows of a 32-lane pass (k rows r..r+7 and r+16..r+23) need
+    // distinct chunks among the 8 rows of each parity: (kr >> 1) & 3 and bit 4 of kr; it is the same
+    // for the rows 8 and 64 apart that a lane's second read and k-group 1 read, and below 8, the
+    // row's chunk count.
     __device__ static inline int swz(int kr) {
-        if constexpr (ES == 1) return (kr & 7) | (((kr >> 4) & 1) << 3);
+        if constexpr (ES == 1 && ROWS == 128) return ((kr >> 1) & 3) | (((kr >> 4) & 1) << 2);
+        else if constexpr (ES == 1) return (kr & 7) | (((kr >> 4) & 1) << 3);
         else return ((kr & 3) | (((kr >> 3) & 1) << 2)) << 1;
     }
 
@@ -1342,13 +1348,13 @@ static int run_modes_dma(const GemmDesc& d, hipStream_t stream, int group_m, boo
         TV_CASE(LOAD_MNCONTIG, LOAD_KCONTIG)
 #undef TV_CASE
     }
-    // 16-bit GEMMs whose 128x128 tiles all fit one round of resident workgroups (two per CU) run
-    // 128x128 tiles: few 256x256 tiles leave CUs idle.  Measured against 256x256 tiles (and their
+    // 16-bit and int8 GEMMs whose 128x128 tiles all fit one round of resident workgroups (two per
+    // CU) run 128x128 tiles: few 256x256 tiles leave CUs idle.  Measured against 256x256 tiles (and their
     // stream-K schedule) on one box: bf16 [1024,4096]@[4096,4096] 45.5 against 62.7 us,
     // [128,8192]@[8192,8192] 43.5 against 79.3, [2048]^3 25.6 against 41.6, [2048,4096]@[4096,4096]
     // 67.4 against 78.6 (512 tiles of 128x128); but [3000,4096]@[4096,4096] (768 of them) 102.6
     // against 83.7.
-    if constexpr (sizeof(T) == 2 && BM == 256 && BN == 256) {
+    if constexpr (BM == 256 && BN == 256) {
         const int64_t tiles128 = (int64_t)((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
         if (am != LOAD_GENERIC && bm != LOAD_GENERIC && tiles128 <= 2 * (int64_t)device_cus()) {
 #define TV_CASE(A_, B_) \

@@ -321,7 +321,7 @@ def test_direct_load_stream_k_bit_exact(hip, dt, batch, M, K, N):
     np.testing.assert_array_equal(to_storage(plain), c)
 
 
-@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16])
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, INT8])
 @pytest.mark.parametrize("batch,M,K,N,a_t,b_t", [
     (0, 2048, 1000, 4096, False, False),  # 512 tiles of 128x128: two per CU, the most on that size
     (0, 130, 8208, 8000, False, False),   # 126 tiles of 128x128 over 129 k-tiles: split (stream-K)
@@ -331,23 +331,30 @@ def test_direct_load_stream_k_bit_exact(hip, dt, batch, M, K, N):
     (0, 2100, 520, 4104, False, True)],
     ids=["t128-512", "t128-split", "t128-batch-AtBt", "t256-153", "t256-At", "t256-Bt"])
 def test_direct_load_tile_size_exact(hip, dt, batch, M, K, N, a_t, b_t):
-    """16-bit GEMMs on the direct-load kernels run 128x128 tiles while those fit one round of
-    resident workgroups (two per CU: at most 512 tiles on 256 CUs) and 256x256 tiles above that.
-    Shapes either side of the switch, ragged in M, N and K, with transposed views (every pitch a
-    whole number of 16-byte chunks, so the direct-load kernels take them).  Integer-valued inputs
-    in [-2, 2]: exact fp32 sums in any order, each rounded once; a second call gives the same bits."""
+    """16-bit and int8 GEMMs on the direct-load kernels run 128x128 tiles while those fit one round
+    of resident workgroups (two per CU: at most 512 tiles on 256 CUs) and 256x256 tiles above that.
+    Shapes either side of the switch, ragged in M, N and K, with transposed views (int8's 128-row
+    M/N-contiguous layout has its own swizzle; int8 rows whose K is not whole 16-byte chunks are
+    copied into padded rows first).  Integer-valued inputs: exact sums in any order, half outputs
+    each rounded once, int8 the low byte; a second call gives the same bits."""
     lead = (batch,) if batch else ()
-    x = ints(22, lead + (M, K), -2, 2)
-    y = ints(23, lead + (K, N), -2, 2)
+    lo, hi = (-8, 8) if dt == INT8 else (-2, 2)
+    x = ints(22, lead + (M, K), lo, hi)
+    y = ints(23, lead + (K, N), lo, hi)
+
+    def enc(v):
+        return v.astype(np.int8) if dt == INT8 else half_bits(v, dt)
 
     def dev(v, transposed):
         if transposed:
-            return to_torch(half_bits(np.ascontiguousarray(np.swapaxes(v, -1, -2)), dt), dt).transpose(-1, -2)
-        return to_torch(half_bits(v, dt), dt)
+            return to_torch(enc(np.ascontiguousarray(np.swapaxes(v, -1, -2))), dt).transpose(-1, -2)
+        return to_torch(enc(v), dt)
 
     ta, tb = dev(x, a_t), dev(y, b_t)
     c = to_storage(hip.gemm(ta, tb))
-    np.testing.assert_array_equal(c, half_bits(np.matmul(x, y), dt))
+    exact = np.matmul(x.astype(np.float64), y.astype(np.float64))
+    want = orc.low_byte(exact.astype(np.int64)) if dt == INT8 else half_bits(exact.astype(np.float32), dt)
+    np.testing.assert_array_equal(c, want)
     np.testing.assert_array_equal(to_storage(hip.gemm(ta, tb)), c)
 
 
