@@ -94,7 +94,8 @@ typedef struct tv_gemm_args {
 } tv_gemm_args;
 
 /* General batched matmul.  Routes M <= 8 shapes to the GEMV kernels when they serve the
- * dtype/layout, everything else to the MFMA GEMM kernels (or the SIMT slow path). */
+ * dtype/layout, and 9 <= M <= 32 to the matrix-core GEMV (16-bit W up to 32 rows, int8 W up to 16,
+ * whole 128-byte strips), everything else to the MFMA GEMM kernels (or the SIMT slow path). */
 int tv_hip_gemm(const tv_gemm_args* args, void* hip_stream);
 
 /* Activations of the fused epilogue (the reference's ops::Relu / Silu / Sigmoid / Tanh). */
@@ -133,9 +134,10 @@ int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_st
  * (M > 8) that tv_hip_gemm splits with its stream-K schedule, whose partial tiles need a
  * workspace, run unsplit here, so their fp32 and 16-bit results can differ from tv_hip_gemm's in
  * the last bits (summation order); every other call, and every int8 call, gives tv_hip_gemm's
- * results bit for bit.  A call whose split needs more returns
- * TV_E_SCRATCH (e.g. M = 8 bf16 needs 2 KiB per (64-column strip, K-slice) pair: c5's
- * x[8,4096] @ W[4096,11008] needs 1.4 MiB).
+ * results bit for bit.  A call whose split needs more returns TV_E_SCRATCH at M <= 8 (e.g. M = 8
+ * bf16 needs 2 KiB per (64-column strip, K-slice) pair: c5's x[8,4096] @ W[4096,11008] needs
+ * 1.4 MiB); at 9 <= M <= 32 it runs the GEMM instead (e.g. M = 32 bf16 on c5's W needs 11 MiB of
+ * partials), whose fp32 and 16-bit results can then differ from tv_hip_gemm's in the last bits.
  * The first call on a GPU looks the array up (hipGetSymbolAddress) and clears its counters with a
  * kernel on hip_stream.  All calls on one GPU share its array: calls that overlap on one GPU (on
  * different streams, or from different threads) race and must be serialised by the caller. */

@@ -89,9 +89,12 @@ int run_gemm(const tv_gemm_args* args, const tvk::GemmDesc& d, hipStream_t s, co
     if (d.batch == 0 || d.M == 0 || d.N == 0) return TV_OK;
     if (mfma_pair(args) && d.K == 0) return tvk::launch_gemm_k0(d, s);
     if (mfma_pair(args)) {
-        if (d.M <= 8) {
+        // Skinny M: the GEMV streams W once (M <= 8 always; 9 <= M <= 32 on the matrix-core GEMV,
+        // which the tiled GEMM is about 1.7x slower than there).  Where it declines the call, or
+        // the caller's fixed split-K buffers are too small above M = 8, the GEMM serves it.
+        if (d.M <= 32) {
             const int rc = tvk::launch_gemv(d, s, fixed);
-            if (rc != TV_E_UNSUPPORTED) return rc;
+            if (rc != TV_E_UNSUPPORTED && !(rc == TV_E_SCRATCH && d.M > 8)) return rc;
         }
         return tvk::launch_gemm_mfma(d, s, fixed == nullptr);
     }

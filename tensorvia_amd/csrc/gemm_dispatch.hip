@@ -36,6 +36,10 @@ static int pad_operand(GemmDesc& d, bool is_a, hipStream_t stream) {
     if (L <= 0 || rows <= 0) return 0;
     const int64_t P = (L + vec - 1) / vec * vec;
     const int64_t nb = d.batch > 1 && s_b != 0 ? d.batch : 1;
+    // The copy's layout must itself pass (a k-tile panel's offsets within 31 bits); nullptr stands
+    // for the workspace's 16-byte aligned base.
+    const int64_t ps_r = s_k == 1 ? P : 1, ps_k = s_k == 1 ? 1 : P, ps_b = nb > 1 ? rows * P : 0;
+    if (pick_mode(nullptr, R, K, ps_r, ps_k, ps_b, d.batch, es, 256, true) == LOAD_GENERIC) return 0;
     void* ws = nullptr;
     if (gemm_pad_workspace(stream, (size_t)(nb * rows * P * es), is_a ? 0 : 1, &ws) != 0) return 0; // no room: gather
     const int rc = launch_pad_rows(p, ws, es, nb, rows, s_row, s_b, L, P, stream);

@@ -315,8 +315,10 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
 //  * the wave writes it to its own LDS tile (32 rows x 64 columns, row pitch 144 bytes) and reads it
 //    back with ds_read_b64_tr_b16, which hands lane l the 8 consecutive rows of one column that the
 //    matrix core's B operand wants (column 16 f + l mod 16, rows 8 (l / 16) ..);
-//  * one v_mfma_f32_16x16x32 per 16 columns: A = x rows 0..15 (rows 8..15 and rows >= M are zero),
-//    so D[m][n] lands in lane n mod 16 + 16 (m / 4), element m mod 4;
+//  * one v_mfma_f32_16x16x32 per 16 columns and 16-row block of x: XR = 8 stages x rows 0..7 (the
+//    block's rows 8..15 are zero), XR = 16 or 32 one or two whole blocks (9 <= M <= 32), rows >= M
+//    zero; D[m][n] of a block lands in lane n mod 16 + 16 (m / 4), element m mod 4, and each W
+//    fragment read from LDS serves every block;
 //  * the waves' partials are summed through LDS in wave order, then published as in gemv_kernel.
 // A wave's LDS tile is private to it: LDS instructions of one wave execute in order, so the next
 // chunk's stores cannot overtake the previous chunk's reads.
@@ -326,20 +328,25 @@ constexpr int kGemvMfmaPitch = 144;
 constexpr int kGemvMfmaWaves = 4;
 template <typename T> constexpr int gemv_mfma_depth() { return sizeof(T) == 2 ? 2 : 1; }
 
-template <typename T, int WAVES, int DEPTH>
+template <typename T, int WAVES, int DEPTH, int XR>
 __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
     using Acc = typename GemvTraits<T>::Acc;
+    static_assert(XR == 8 || XR == 16 || XR == 32, "x rows staged: 8 (M <= 8), 16 or 32");
+    constexpr int MB = XR < 16 ? 1 : XR / 16; // 16-row blocks of x
     // 16-bit: 64-column strips, 32-row chunks (v_mfma_f32_16x16x32, ds_read_b64_tr_b16); int8:
     // 128-column strips, 64-row chunks (v_mfma_i32_16x16x64_i8, ds_read_b64_tr_b8).
     constexpr int ES = sizeof(T), VEC = 16 / ES, NB = 8 * VEC, CH = 64 / ES, NQ = CH / 8, NF = NB / 16;
     constexpr int PITCH = kGemvMfmaPitch, THREADS = WAVES * 64;
     static_assert(ES == 1 || ES == 2, "16-bit or 8-bit W");
-    static_assert(8 * NB % THREADS == 0, "outputs per thread");
+    static_assert(XR * NB % THREADS == 0, "outputs per thread");
     const GemmDesc& d = g.d;
 
-    extern __shared__ __attribute__((aligned(16))) char xs[]; // 8 rows x kpad x ES (launch size)
+    // x's rows (XR x kpad x ES, the launch size), and for XR > 8 also the wave partials after the
+    // loop (the launch sizes the area for both: gemv_mfma_dyn_lds); XR = 8 keeps its own array.
+    extern __shared__ __attribute__((aligned(16))) char xs[];
     __shared__ __attribute__((aligned(16))) char wt[WAVES][CH * PITCH];
-    __shared__ Acc red[WAVES][8][NB];
+    constexpr bool kRedInX = XR > 8;
+    __shared__ Acc red_own[kRedInX ? 1 : WAVES][kRedInX ? 1 : XR][NB];
     __shared__ int last_flag;
 
     // The wave index from the first lane: wave-uniform to the compiler, so the loop below has scalar
@@ -379,41 +386,43 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
 #pragma unroll
     for (int j = 0; j < DEPTH; ++j) issue(j, j);
 
-    // x[b][0..8)[k0 .. k0 + kpad) in LDS; rows >= M and columns >= ks are zero.  Four chunks per
+    // x[b][0..XR)[k0 .. k0 + kpad) in LDS; rows >= M and columns >= ks are zero.  Four chunks per
     // thread are loaded before any is stored: each wait for an x load also waits for the W loads
     // issued before it, so the loads go out together and pay that wait once.
     {
         const char* xb = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + k0) * ES;
         const int cpr = kpad * ES / 16;
-        for (int i0 = tid; i0 < 8 * cpr; i0 += 4 * THREADS) {
+        for (int i0 = tid; i0 < XR * cpr; i0 += 4 * THREADS) {
             u32x4 v[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int i = i0 + u * THREADS, m = i / cpr, c = i - m * cpr;
                 v[u] = u32x4{0, 0, 0, 0};
-                if (i < 8 * cpr && m < d.M && c * 16 < ks * ES)
+                if (i < XR * cpr && m < d.M && c * 16 < ks * ES)
                     v[u] = *reinterpret_cast<const u32x4*>(xb + (int64_t)m * d.sa_m * ES + c * 16);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int i = i0 + u * THREADS;
-                if (i < 8 * cpr) *reinterpret_cast<u32x4*>(xs + i * 16) = v[u];
+                if (i < XR * cpr) *reinterpret_cast<u32x4*>(xs + i * 16) = v[u];
             }
         }
     }
     __syncthreads();
 
-    typename Mfma<T>::Acc acc[NF];
+    typename Mfma<T>::Acc acc[MB][NF];
 #pragma unroll
-    for (int f = 0; f < NF; ++f) acc[f] = typename Mfma<T>::Acc{0, 0, 0, 0};
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) acc[mb][f] = typename Mfma<T>::Acc{0, 0, 0, 0};
     char* wl = wt[wave];
     const int wr_off = r0 * PITCH + cc * 16;
     // transpose reads: 16-bit, lanes 4r + c of a 16-lane group read row kb + r, columns 4c .. 4c + 3
     // (then rows + 4); 8-bit, lanes 2r + c read row kb + r, columns 8c .. 8c + 7 (then rows + 8)
     const int fr = lane & 15, kb = (lane >> 4) * (CH / 4);
     const int rd_off = ES == 2 ? (kb + (fr >> 2)) * PITCH + 8 * (fr & 3) : (kb + (fr >> 1)) * PITCH + 8 * (fr & 1);
-    const bool arow = fr < 8;
-    const char* xa = xs + (lane & 7) * kpad * ES + kb * ES;
+    const bool arow = XR > 8 || fr < 8;
+    const char* xa = xs + (XR > 8 ? fr : (lane & 7)) * kpad * ES + kb * ES; // block mb: + 16 mb rows
     // No per-chunk guard: the step count is a multiple of DEPTH, and a chunk past niter multiplies
     // zeros (its W loads are out of range, its x fragment is zeroed).
     for (int j0 = 0; j0 < nsteps; j0 += DEPTH) {
@@ -424,8 +433,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
                 const int c = wave + WAVES * j;
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) *reinterpret_cast<u32x4*>(wl + wr_off + q * 8 * PITCH) = w[dd][q];
-                u32x4 a = *reinterpret_cast<const u32x4*>(xa + (j < niter ? c : 0) * CH * ES);
-                if (!arow || j >= niter) a = u32x4{0, 0, 0, 0};
+                u32x4 a[MB];
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    a[mb] = *reinterpret_cast<const u32x4*>(xa + (mb * 16 * kpad + (j < niter ? c : 0) * CH) * ES);
+                    if (!arow || j >= niter) a[mb] = u32x4{0, 0, 0, 0};
+                }
 #pragma unroll
                 for (int f = 0; f < NF; ++f) {
                     const lds_char* p = (const lds_char*)(wl + rd_off + f * 16 * ES);
@@ -440,21 +453,26 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
                         const i32x2_t hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(p + 8 * PITCH));
                         bf = u32x4{(unsigned)lo.x, (unsigned)lo.y, (unsigned)hi.x, (unsigned)hi.y};
                     }
-                    Mfma<T>::run(a, bf, acc[f]);
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) Mfma<T>::run(a[mb], bf, acc[mb][f]);
                 }
                 issue(dd, j + DEPTH); // out of range past niter: zeros
             }
         }
     }
 
-    // Wave partials D[m][n] (m < 8: lanes 0..31) to red, then sum the waves in order.
-    if (lane < 32)
+    // Wave partials D[m][n] (XR = 8: rows 0..7, lanes 0..31) to red, then sum the waves in order.
+    if constexpr (kRedInX) __syncthreads(); // every wave is done reading x
+    Acc(*red)[XR][NB] = kRedInX ? reinterpret_cast<Acc(*)[XR][NB]>(xs) : reinterpret_cast<Acc(*)[XR][NB]>(&red_own[0][0][0]);
+    if (XR > 8 || lane < 32)
 #pragma unroll
-        for (int f = 0; f < NF; ++f)
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) red[wave][4 * (lane >> 4) + r][16 * f + (lane & 15)] = acc[f][r];
+            for (int f = 0; f < NF; ++f)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[wave][16 * mb + 4 * (lane >> 4) + r][16 * f + (lane & 15)] = acc[mb][f][r];
     __syncthreads();
-    constexpr int OPT = 8 * NB / THREADS; // outputs per thread
+    constexpr int OPT = XR * NB / THREADS; // outputs per thread
     Acc v[OPT];
 #pragma unroll
     for (int i = 0; i < OPT; ++i) {
@@ -477,14 +495,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
         return;
     }
 
-    // Publish slot s of this strip ([8][NB] accumulators, fp32 or int32, rows < M), count in; the
+    // Publish slot s of this strip ([XR][NB] accumulators, fp32 or int32, rows < M), count in; the
     // last arriver sums the slots in order.
     const int strip = lin;
-    Acc* slots = static_cast<Acc*>(g.part) + (int64_t)strip * g.nslices * 8 * NB;
+    Acc* slots = static_cast<Acc*>(g.part) + (int64_t)strip * g.nslices * XR * NB;
 #pragma unroll
     for (int i = 0; i < OPT; ++i)
         if ((tid + THREADS * i) / NB < d.M)
-            __hip_atomic_store(slots + (int64_t)s * 8 * NB + tid + THREADS * i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(slots + (int64_t)s * XR * NB + tid + THREADS * i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     publish_and_count(g.cnt + strip, g.nslices, &last_flag);
     if (!last_flag) return;
 #pragma unroll
@@ -494,7 +512,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
             Acc part_v[kGemvMaxSlices];
 #pragma unroll
             for (int k = 0; k < kGemvMaxSlices; ++k)
-                part_v[k] = k < g.nslices ? __hip_atomic_load(slots + (int64_t)k * 8 * NB + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                part_v[k] = k < g.nslices ? __hip_atomic_load(slots + (int64_t)k * XR * NB + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                                           : Acc(0);
             Acc t = part_v[0];
 #pragma unroll
@@ -607,7 +625,7 @@ static bool gemv_layout_ok(const GemmDesc& d) {
     const int es = (int)dtype_size(d.dtype_a);
     const int64_t vec = 16 / es;
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-    if (d.M < 1 || d.M > 8) return false;
+    if (d.M < 1 || d.M > 32) return false; // M > 8: the matrix-core kernel only (launch_gemv)
     if (d.sb_n != 1 || !al(d.B) || d.N % vec || (d.K > 1 && d.sb_k % vec) || (d.batch > 1 && d.sb_b % vec)) return false;
     if (d.sa_k != 1 || !al(d.A) || d.K % vec || (d.M > 1 && d.sa_m % vec) || (d.batch > 1 && d.sa_b % vec)) return false;
     if (d.K > 1 && d.sb_k < d.N) return false;
@@ -680,22 +698,32 @@ static int gemv_run(const GemmDesc& d, hipStream_t stream, int nslices, const Ge
     return hipGetLastError();
 }
 
+// Dynamic LDS of the matrix-core GEMV: x's XR rows of kpad, and for XR > 8 at least the wave
+// partials, which reuse that area after the loop.
+template <typename T, int XR, int WAVES = kGemvMfmaWaves>
+static size_t gemv_mfma_dyn_lds(int kpad) {
+    const size_t x = (size_t)XR * kpad * sizeof(T);
+    const size_t red = XR > 8 ? (size_t)WAVES * XR * (128 / sizeof(T)) * sizeof(typename GemvTraits<T>::Acc) : 0;
+    return x > red ? x : red;
+}
+
 // K slices of the matrix-core GEMV asked for as `nslices`: at least what x's LDS slice needs, rows
 // per slice a multiple of the 16-byte vector; S is what the rounding leaves.
 struct GemvSlices {
     int S, kslice, kpad;
 };
-template <typename T, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
+template <typename T, int XR, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
 static GemvSlices gemv_mfma_slices(const GemmDesc& d, int nslices) {
     using Acc = typename GemvTraits<T>::Acc;
     constexpr int ES = sizeof(T), VEC = 16 / ES, NB = 8 * VEC, CH = 64 / ES;
-    // A workgroup's LDS (at most 160 KB) holds the kernel's static arrays and x's rows of a slice:
-    // x rows per slice are capped by both gemv_kcap and what the static arrays leave.
+    // A workgroup's LDS (at most 160 KB) holds the kernel's static arrays and x's XR rows of a
+    // slice: x rows per slice are capped by kGemvXBytes and by what the static arrays leave.
     constexpr int kLds = 160 * 1024;
-    constexpr int kStatic = WAVES * CH * kGemvMfmaPitch + WAVES * 8 * NB * (int)sizeof(Acc) + 16;
-    static_assert(kStatic + 8 * ES * CH <= kLds, "static LDS leaves no room for x");
-    constexpr int kFit = (kLds - kStatic) / (8 * ES) / CH * CH;
-    constexpr int KCAP = gemv_kcap<T>() < kFit ? gemv_kcap<T>() : kFit; // a multiple of CH
+    constexpr int kStatic = WAVES * CH * kGemvMfmaPitch + (XR > 8 ? 0 : WAVES * XR * NB * (int)sizeof(Acc)) + 16;
+    static_assert(kStatic + XR * ES * CH <= kLds, "static LDS leaves no room for x");
+    constexpr int kFit = (kLds - kStatic) / (XR * ES) / CH * CH;
+    constexpr int kX = kGemvXBytes / (XR * ES) / CH * CH;
+    constexpr int KCAP = kX < kFit ? kX : kFit; // a multiple of CH
     int S = nslices < 1 ? 1 : nslices;
     const int min_s = (d.K + KCAP - 1) / KCAP;
     if (S < min_s) S = min_s;
@@ -707,13 +735,13 @@ static GemvSlices gemv_mfma_slices(const GemmDesc& d, int nslices) {
 }
 
 // The matrix-core GEMV (bf16 / fp16 with 64-column strips, int8 with 128-column strips).
-template <typename T, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
+template <typename T, int XR, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
 static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices, const GemvScratch* fixed) {
     using Acc = typename GemvTraits<T>::Acc;
     constexpr int ES = sizeof(T), VEC = 16 / ES, NB = 8 * VEC;
     if (d.K < 1) return TV_E_UNSUPPORTED;
     const int nblk = (d.N + NB - 1) / NB;
-    const GemvSlices sl = gemv_mfma_slices<T, WAVES, DEPTH>(d, nslices);
+    const GemvSlices sl = gemv_mfma_slices<T, XR, WAVES, DEPTH>(d, nslices);
     const int S = sl.S, kslice = sl.kslice;
     if (S > kGemvMaxSlices) return TV_E_UNSUPPORTED;
     if ((int64_t)(kslice - 1) * d.sb_k * ES + (int64_t)d.N * ES >= ((int64_t)1 << 30)) return TV_E_UNSUPPORTED;
@@ -728,17 +756,18 @@ static int gemv_mfma_run(const GemmDesc& d, hipStream_t stream, int nslices, con
     g.cnt = nullptr;
     g.part = nullptr;
     if (S > 1) {
-        const int rc = split_buffers(stream, fixed, nwg, (size_t)nwg * S * 8 * NB * sizeof(Acc), g);
+        const int rc = split_buffers(stream, fixed, nwg, (size_t)nwg * S * XR * NB * sizeof(Acc), g);
         if (rc) return rc;
     }
-    hipLaunchKernelGGL((gemv_mfma_kernel<T, WAVES, DEPTH>), dim3((unsigned)nwg, S), dim3(WAVES * 64), (size_t)8 * sl.kpad * ES, stream, g);
+    const size_t lds = gemv_mfma_dyn_lds<T, XR, WAVES>(sl.kpad);
+    hipLaunchKernelGGL((gemv_mfma_kernel<T, WAVES, DEPTH, XR>), dim3((unsigned)nwg, S), dim3(WAVES * 64), lds, stream, g);
     return hipGetLastError();
 }
 
 // Workgroups of the matrix-core GEMV that the current device holds at once: resident workgroups
 // per CU at the launch's LDS size (the occupancy API) times the CUs.  Cached per device and LDS
 // size (x's slice is the only part that varies); 0 if the runtime cannot tell.
-template <typename T, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
+template <typename T, int XR, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
 static int64_t gemv_mfma_capacity(int kpad) {
     static std::mutex mu;
     static std::map<std::pair<int, int>, int64_t> cache;
@@ -749,8 +778,8 @@ static int64_t gemv_mfma_capacity(int kpad) {
     const auto it = cache.find(key);
     if (it != cache.end()) return it->second;
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(gemv_mfma_kernel<T, WAVES, DEPTH>),
-                                                     WAVES * 64, (size_t)8 * kpad * sizeof(T)) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(gemv_mfma_kernel<T, WAVES, DEPTH, XR>),
+                                                     WAVES * 64, gemv_mfma_dyn_lds<T, XR, WAVES>(kpad)) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 0;
     const int64_t cap = (int64_t)(per_cu > 0 ? per_cu : 0) * (cus > 0 ? cus : 0);
@@ -793,7 +822,7 @@ static int launch_gemv_plan_with(const GemmDesc& d, hipStream_t stream, const Ge
 }
 
 int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices) {
-    if (!gemv_layout_ok(d)) return TV_E_UNSUPPORTED;
+    if (!gemv_layout_ok(d) || d.M > 8) return TV_E_UNSUPPORTED; // the dot-product kernel: M <= 8
     if (d.N == 0 || d.batch == 0) return 0;
     return launch_gemv_plan_with(d, stream, GemvPlan{nl, threads, nslices}, nullptr);
 }
@@ -813,7 +842,7 @@ int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads,
 //  * under 0.6 of a round.
 // It then takes the nearest slice count (more slices first) that avoids all three.  The resident
 // capacity comes from the occupancy API at the launch's LDS size.
-template <typename T>
+template <typename T, int XR>
 static int gemv_mfma_pick(const GemmDesc& d) {
     constexpr int ES = sizeof(T), NB = 128 / ES, CH = 64 / ES;
     const int64_t strips = (int64_t)(d.N + NB - 1) / NB * d.batch;
@@ -822,10 +851,10 @@ static int gemv_mfma_pick(const GemmDesc& d) {
     const int64_t target = ES == 2 ? 688 : 344;
     int s0 = (int)((target + strips - 1) / strips);
     if (s0 > max_s) s0 = max_s;
-    s0 = gemv_mfma_slices<T>(d, s0).S; // raised to what x's LDS slice needs
+    s0 = gemv_mfma_slices<T, XR>(d, s0).S; // raised to what x's LDS slice needs
 
     static std::mutex mu;
-    static std::map<std::tuple<int, int64_t, int>, int> picked; // (device, strips, K) -> S
+    static std::map<std::tuple<int, int64_t, int>, int> picked; // (device, strips, K) -> S, per XR
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return s0;
     const auto key = std::make_tuple(dev, strips, d.K);
@@ -841,9 +870,9 @@ static int gemv_mfma_pick(const GemmDesc& d) {
     int s_of[kGemvMaxSlices + 2] = {};
     int occ_best = 0;
     for (int s = 1; s <= top && s <= kGemvMaxSlices; ++s) {
-        const GemvSlices sl = gemv_mfma_slices<T>(d, s);
+        const GemvSlices sl = gemv_mfma_slices<T, XR>(d, s);
         s_of[s] = sl.S;
-        cap[s] = gemv_mfma_capacity<T>(sl.kpad);
+        cap[s] = gemv_mfma_capacity<T, XR>(sl.kpad);
         if (cap[s] <= 0) return s0;
         const int occ = (int)(cap[s] / cus);
         if (occ > occ_best) occ_best = occ;
@@ -866,19 +895,31 @@ static int gemv_mfma_pick(const GemmDesc& d) {
     return S;
 }
 
+template <typename T, int XR>
+static int gemv_mfma_go(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed) {
+    return gemv_mfma_run<T, XR>(d, stream, gemv_mfma_pick<T, XR>(d), fixed);
+}
+// x rows staged: 8 up to M = 8 (c5's kernel), then whole 16-row blocks: 16, and 32 at 16 bits (in
+// int8 the 128-column strips' wave partials for 32 rows would take 64 KB of LDS).
 static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed) {
     switch (d.dtype_a) {
-        case TV_BFLOAT16: return gemv_mfma_run<__bf16>(d, stream, gemv_mfma_pick<__bf16>(d), fixed);
-        case TV_FLOAT16: return gemv_mfma_run<_Float16>(d, stream, gemv_mfma_pick<_Float16>(d), fixed);
-        default: return gemv_mfma_run<int8_t>(d, stream, gemv_mfma_pick<int8_t>(d), fixed);
+        case TV_BFLOAT16:
+            return d.M <= 8 ? gemv_mfma_go<__bf16, 8>(d, stream, fixed) : d.M <= 16 ? gemv_mfma_go<__bf16, 16>(d, stream, fixed)
+                                                                                    : gemv_mfma_go<__bf16, 32>(d, stream, fixed);
+        case TV_FLOAT16:
+            return d.M <= 8 ? gemv_mfma_go<_Float16, 8>(d, stream, fixed) : d.M <= 16 ? gemv_mfma_go<_Float16, 16>(d, stream, fixed)
+                                                                                      : gemv_mfma_go<_Float16, 32>(d, stream, fixed);
+        default: return d.M <= 8 ? gemv_mfma_go<int8_t, 8>(d, stream, fixed) : gemv_mfma_go<int8_t, 16>(d, stream, fixed);
     }
 }
 
 int launch_gemv(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed) {
     if (!gemv_layout_ok(d)) return TV_E_UNSUPPORTED;
     if (d.N == 0 || d.batch == 0) return 0;
-    if ((d.dtype_a == TV_BFLOAT16 || d.dtype_a == TV_FLOAT16 || (d.dtype_a == TV_INT8 && d.M >= 3)) && gemv_nl(d) == 8)
-        return launch_gemv_mfma(d, stream, fixed);
+    const bool mfma = (d.dtype_a == TV_BFLOAT16 || d.dtype_a == TV_FLOAT16 || (d.dtype_a == TV_INT8 && d.M >= 3)) && gemv_nl(d) == 8;
+    if (d.M > 8) // 9 <= M <= 32: the matrix-core kernel only (16-bit up to 32 rows, int8 up to 16)
+        return mfma && (d.dtype_a != TV_INT8 || d.M <= 16) ? launch_gemv_mfma(d, stream, fixed) : TV_E_UNSUPPORTED;
+    if (mfma) return launch_gemv_mfma(d, stream, fixed);
     return launch_gemv_plan_with(d, stream, gemv_plan(d), fixed);
 }
 

@@ -1,5 +1,6 @@
 """GPU parity of the skinny-M (decode) path: x[M<=8, K] @ W[K, N] through tv_hip_gemv, against the
-oracle (mul_kernel_basic restated, which is what the reference runs for these shapes)."""
+oracle (mul_kernel_basic restated, which is what the reference runs for these shapes), and
+9 <= M <= 32 on the matrix-core GEMV through tv_hip_gemm."""
 import numpy as np
 import pytest
 import torch
@@ -53,6 +54,30 @@ def test_gemv_integer_inputs_exact(hip, dt, M, KN):
     c = to_storage(hip.gemv(to_torch(xs, dt), to_torch(ws, dt)))
     want = ref if dt == FLOAT32 else half_bits(ref, dt)
     np.testing.assert_array_equal(c, want)
+
+
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, INT8])
+@pytest.mark.parametrize("M", [9, 16, 17, 32])
+@pytest.mark.parametrize("KN", [(4096, 11008), (4000, 1008), (208, 144)])
+def test_skinny_m_matrix_core_exact(hip, dt, M, KN):
+    """9 <= M <= 32 through tv_hip_gemm: the matrix-core GEMV with 16 or 32 rows of x staged (16-bit
+    up to 32 rows, int8 up to 16; int8 at M = 17 and 32 runs the GEMM instead), split over K
+    slices or not, ragged K and N.  Integer-valued inputs: exact sums (half outputs rounded once,
+    int8 the low byte, and int32 outputs the sums themselves)."""
+    K, N = KN
+    if dt == INT8:
+        x = rng.uniform_int(34, M * K, -128, 127).astype(np.int8).reshape(M, K)
+        w = rng.uniform_int(35, K * N, -128, 127).astype(np.int8).reshape(K, N)
+        exact = orc.exact_int(x, w)
+        c = to_storage(hip.gemm(to_torch(x, INT8), to_torch(w, INT8)))
+        c32 = to_storage(hip.gemm(to_torch(x, INT8), to_torch(w, INT8), out_dtype=INT32))
+        np.testing.assert_array_equal(c, exact.astype(np.int8))
+        np.testing.assert_array_equal(c32, exact.astype(np.int32))
+        return
+    x = rng.uniform_int(36, M * K, -2, 2).astype(np.float32).reshape(M, K)
+    w = rng.uniform_int(37, K * N, -2, 2).astype(np.float32).reshape(K, N)
+    c = to_storage(hip.gemm(to_torch(half_bits(x, dt), dt), to_torch(half_bits(w, dt), dt)))
+    np.testing.assert_array_equal(c, half_bits(np.matmul(x, w), dt))
 
 
 @pytest.mark.parametrize("dt,M,K,N", [(BFLOAT16, 1, 4096, 14336), (BFLOAT16, 8, 8192, 28672), (INT8, 8, 8192, 28672),
