@@ -95,8 +95,8 @@ KERNEL = {
     "c3": "gemm_dma_chain_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>> (chained tiles)",
     "c3_fused": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, true>",
     "c4": "gemm_smallk_pipe_kernel<GemmCfg<_Float16, 128, 128, 2, 4, 0, 0>, _Float16> (row-synchronous groups)",
-    "c5m1": "gemv_mfma_kernel<__bf16, 4, 2>",
-    "c5m8": "gemv_mfma_kernel<__bf16, 4, 2>",
+    "c5m1": "gemv_mfma_kernel<__bf16, 4, 2, 8>",
+    "c5m8": "gemv_mfma_kernel<__bf16, 4, 2, 8>",
 }
 # The same kernels as they appear in a rocprofv3 kernel trace (demangled, or mangled where the
 # profiler's demangler gives up on __bf16 / _Float16 template arguments).
