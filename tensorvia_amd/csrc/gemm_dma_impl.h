@@ -1200,9 +1200,12 @@ static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int ti
     if (nk < 64 && ntiles * 5 > G) return 1;
     const int64_t iters = ntiles * nk;
     if (iters / 8 < G) G = (int)(iters / 8);
-    // At most about four segments per tile: bf16 [256,4096]@[4096,4096] (64 tiles of 128x128)
-    // 24.5 us in 4 against 32.0 in 8 and 28.7 in 2, [128,8192]@[8192,8192] 39.7 against 44.9 in 8.
-    if (4 * ntiles < G) G = (int)(4 * ntiles);
+    // At most about four segments per tile, unless the segments stay at least 32 k-tiles long:
+    // bf16 [256,4096]@[4096,4096] (64 tiles of 128x128) 24.5 us in 4 against 32.0 in 8 and 28.7 in
+    // 2, [128,8192]@[8192,8192] 39.7 against 44.9 in 8; a single tile over K = 65536 keeps 32
+    // workgroups rather than 4.
+    const int64_t cap = 4 * ntiles > iters / 32 ? 4 * ntiles : iters / 32;
+    if (cap < G) G = (int)cap;
     if (G < 1) return 1;
     SkArgs sk;
     sk.iters = iters;
