@@ -878,7 +878,9 @@ static int run_cfg_sk(const GemmDesc& d, hipStream_t stream, int group_m, int ti
     // Whole rounds of G tiles run whole; only the last, partial round is split.
     const int64_t dp = ntiles > G ? ntiles / G * G : 0;
     const int64_t iters = (ntiles - dp) * nk;
-    const int wgs = (int)(iters / 8 < G ? iters / 8 : G);
+    int wgs = (int)(iters / 8 < G ? iters / 8 : G);
+    // At most 32 segments per split tile: a tile's last-arriving workgroup sums its slots alone.
+    if (32 * (ntiles - dp) < wgs) wgs = (int)(32 * (ntiles - dp));
     if (dp == 0) G = wgs;
     if (G < 1) return 1;
     SkArgs sk;
