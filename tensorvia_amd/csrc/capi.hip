@@ -85,9 +85,14 @@ int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
 // Routing shared by tv_hip_gemm, tv_hip_gemm_ex and tv_hip_gemm_noalloc (fixed: the GEMV's
 // split-K buffers, nullptr for the per-stream workspace; with fixed buffers the GEMM takes no
 // schedule that needs a workspace either).
-int run_gemm(const tv_gemm_args* args, const tvk::GemmDesc& d, hipStream_t s, const tvk::GemvScratch* fixed = nullptr) {
-    if (d.batch == 0 || d.M == 0 || d.N == 0) return TV_OK;
-    if (mfma_pair(args) && d.K == 0) return tvk::launch_gemm_k0(d, s);
+int run_gemm(const tv_gemm_args* args, const tvk::GemmDesc& d0, hipStream_t s, const tvk::GemvScratch* fixed = nullptr) {
+    if (d0.batch == 0 || d0.M == 0 || d0.N == 0) return TV_OK;
+    if (mfma_pair(args) && d0.K == 0) return tvk::launch_gemm_k0(d0, s);
+    tvk::GemmDesc d = d0;
+    if (mfma_pair(args) && fixed == nullptr) { // misaligned operands into padded rows (workspace)
+        const int rc = tvk::pad_gemm_operands(d, s);
+        if (rc) return rc;
+    }
     if (mfma_pair(args)) {
         // Skinny M: the GEMV streams W once (M <= 8 always; 9 <= M <= 32 on the matrix-core GEMV,
         // which the tiled GEMM is about 1.7x slower than there).  Where it declines the call, or

@@ -11,8 +11,8 @@ int launch_gemm_mfma_i8(const GemmDesc& d, hipStream_t stream, bool may_alloc);
 // pitch, batch stride or base address) would be read by the element-gather loader, one load per
 // element: bf16 [2048,4096] @ [4096,4100] took 1.18 ms that way, against about 0.1 ms on the
 // vector loaders.  With a workspace, such an operand is copied once into rows of whole chunks, zero
-// past its valid extent (pad_a / pad_b tell the load-mode choice that the tail may be read), and
-// the GEMM runs on the copy.  Small GEMMs keep the gather (the copy would be the larger cost).
+// past its valid extent (pad_a / pad_b tell the load-mode choice, and the matrix-core GEMV, that
+// the tail may be read), and the call runs on the copy.  Small calls keep the gather.
 static int pad_operand(GemmDesc& d, bool is_a, hipStream_t stream) {
     const int es = (int)dtype_size(is_a ? d.dtype_a : d.dtype_b);
     if (es != 1 && es != 2 && es != 4) return 0;
@@ -20,6 +20,7 @@ static int pad_operand(GemmDesc& d, bool is_a, hipStream_t stream) {
     const void* p = is_a ? d.A : d.B;
     const int64_t R = is_a ? d.M : d.N, K = d.K;
     const int64_t s_r = is_a ? d.sa_m : d.sb_n, s_k = is_a ? d.sa_k : d.sb_k, s_b = is_a ? d.sa_b : d.sb_b;
+    if (is_a ? d.pad_a : d.pad_b) return 0; // already a padded copy
     if (pick_mode(p, R, K, s_r, s_k, s_b, d.batch, es, 256, false) != LOAD_GENERIC) return 0;
     int64_t L, rows, s_row;
     if (s_k == 1) { // rows (m / n) of L = K contiguous elements
@@ -58,16 +59,20 @@ static int pad_operand(GemmDesc& d, bool is_a, hipStream_t stream) {
     return 0;
 }
 
-// GEMMs of at least this many multiply-adds copy misaligned operands (pad_operand).
-constexpr int64_t kPadMinMacs = (int64_t)1 << 24;
+// Calls of at least this many multiply-adds, or of K at least kPadMinK, copy misaligned operands
+// (pad_operand): below both the gather is cheaper than a second launch.  The gather's cost grows
+// with K per output tile (about 4 us per 64 k of bf16), not with the work: bf16 x[1,4096] @
+// W[4096,129] (0.5 M) took 276 us gathered, against about 20 us copied onto the matrix-core GEMV.
+constexpr int64_t kPadMinMacs = (int64_t)1 << 20;
+constexpr int kPadMinK = 256;
 
-int launch_gemm_mfma(const GemmDesc& d0, hipStream_t stream, bool may_alloc) {
-    GemmDesc d = d0;
-    if (may_alloc && (int64_t)d.M * d.N * d.K * (d.batch > 1 ? d.batch : 1) >= kPadMinMacs) {
-        int rc = pad_operand(d, true, stream);
-        if (rc == 0) rc = pad_operand(d, false, stream);
-        if (rc) return rc;
-    }
+int pad_gemm_operands(GemmDesc& d, hipStream_t stream) {
+    if ((int64_t)d.M * d.N * d.K * (d.batch > 1 ? d.batch : 1) < kPadMinMacs && d.K < kPadMinK) return 0;
+    const int rc = pad_operand(d, true, stream);
+    return rc ? rc : pad_operand(d, false, stream);
+}
+
+int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream, bool may_alloc) {
     switch (d.dtype_a) {
         case TV_FLOAT32: return launch_gemm_mfma_f32(d, stream, may_alloc);
         case TV_BFLOAT16: return launch_gemm_mfma_bf16(d, stream, may_alloc);

@@ -359,7 +359,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
     const int n0 = (lin - b * g.nblk) * NB;
     const int s = blockIdx.y;
     const int k0 = s * g.kslice;
-    const int ks = min(d.K - k0, g.kslice);  // a multiple of VEC
+    const int ks = min(d.K - k0, g.kslice);  // a multiple of VEC, except the last slice of a padded x
     const int nch = (ks + CH - 1) / CH;
     const int kpad = nch * CH;
     const int niter = (nch - wave + WAVES - 1) / WAVES; // chunks wave, wave + WAVES, ...
@@ -367,10 +367,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
 
     const int64_t rowb = d.sb_k * ES;
     const char* wbase = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)k0 * d.sb_k) * ES;
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wbase, (int64_t)(ks - 1) * rowb + (int64_t)d.N * ES);
+    // The last row's range ends at N rounded up to whole chunks (N itself unless W is a padded copy).
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wbase, (int64_t)(ks - 1) * rowb + (int64_t)((d.N + VEC - 1) / VEC * VEC) * ES);
     const int r0 = lane >> 3, cc = lane & 7;
     const int col = n0 + cc * VEC;
-    const bool col_ok = col < d.N; // N % VEC == 0 is a launch precondition
+    const bool col_ok = col < d.N; // a chunk straddling N (padded copy) reads the zero padding
     const unsigned colb = (unsigned)(col * ES);
 
     u32x4 w[DEPTH][NQ];
@@ -626,8 +627,10 @@ static bool gemv_layout_ok(const GemmDesc& d) {
     const int64_t vec = 16 / es;
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     if (d.M < 1 || d.M > 32) return false; // M > 8: the matrix-core kernel only (launch_gemv)
-    if (d.sb_n != 1 || !al(d.B) || d.N % vec || (d.K > 1 && d.sb_k % vec) || (d.batch > 1 && d.sb_b % vec)) return false;
-    if (d.sa_k != 1 || !al(d.A) || d.K % vec || (d.M > 1 && d.sa_m % vec) || (d.batch > 1 && d.sa_b % vec)) return false;
+    // N and K need not be whole chunks on zero-padded copies (pad_b / pad_a); launch_gemv keeps such
+    // calls on the matrix-core kernel.
+    if (d.sb_n != 1 || !al(d.B) || (d.N % vec && !d.pad_b) || (d.K > 1 && d.sb_k % vec) || (d.batch > 1 && d.sb_b % vec)) return false;
+    if (d.sa_k != 1 || !al(d.A) || (d.K % vec && !d.pad_a) || (d.M > 1 && d.sa_m % vec) || (d.batch > 1 && d.sa_b % vec)) return false;
     if (d.K > 1 && d.sb_k < d.N) return false;
     return true;
 }
@@ -917,6 +920,8 @@ int launch_gemv(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed)
     if (!gemv_layout_ok(d)) return TV_E_UNSUPPORTED;
     if (d.N == 0 || d.batch == 0) return 0;
     const bool mfma = (d.dtype_a == TV_BFLOAT16 || d.dtype_a == TV_FLOAT16 || (d.dtype_a == TV_INT8 && d.M >= 3)) && gemv_nl(d) == 8;
+    const int64_t vec = 16 / (int64_t)dtype_size(d.dtype_a);
+    if ((d.N % vec || d.K % vec) && !mfma) return TV_E_UNSUPPORTED; // padded ragged N / K: matrix-core kernel only
     if (d.M > 8) // 9 <= M <= 32: the matrix-core kernel only (16-bit up to 32 rows, int8 up to 16)
         return mfma && (d.dtype_a != TV_INT8 || d.M <= 16) ? launch_gemv_mfma(d, stream, fixed) : TV_E_UNSUPPORTED;
     if (mfma) return launch_gemv_mfma(d, stream, fixed);

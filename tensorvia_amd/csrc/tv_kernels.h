@@ -46,7 +46,7 @@ struct GemmDesc {
     int64_t sbias_b = 0, sbias_m = 0, sbias_n = 0; // element strides (0 broadcasts), non-negative
     int64_t bias_bytes = 0;                        // extent of the bias read (below 2^30)
     int32_t act = TV_ACT_NONE;
-    // 1: the operand is a copy made by launch_gemm_mfma whose rows are whole 16-byte chunks, zero
+    // 1: the operand is a copy made by pad_gemm_operands whose rows are whole 16-byte chunks, zero
     // past the valid extent, so a chunk that straddles the end of the valid extent may be read.
     int32_t pad_a = 0, pad_b = 0;
 };
@@ -158,6 +158,10 @@ inline int pick_mode(const void* p, int64_t R, int64_t K, int64_t s_r, int64_t s
 // may_alloc = false: no launch path that needs a grown workspace (the stream-K schedule of the fp32
 // kernel); the plain data-parallel kernels serve the call.
 int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream, bool may_alloc = true);
+// Copies operands that are contiguous along one dimension but not in whole 16-byte rows into
+// zero-padded rows in the per-stream workspace (calls of at least 2^20 multiply-adds or K >= 256) and points d
+// at the copies (pad_a / pad_b).  0 with d unchanged when nothing needs or gets a copy.
+int pad_gemm_operands(GemmDesc& d, hipStream_t stream);
 // Per-(device, stream) buffers of the stream-K GEMM schedule: `cnt_ints` arrival counters (zero
 // between launches) and `slot_bytes` of partial-accumulator slots.
 int gemm_sk_workspace(hipStream_t stream, size_t cnt_ints, size_t slot_bytes, int** cnt, char** slots);

@@ -398,14 +398,20 @@ def test_direct_load_chain_transposed_views(hip, dt, a_t, b_t):
     (0, 1000, 700, 1030, False, False, False),  # A's rows (K) and B's k rows (N) not whole 16-byte chunks
     (0, 1030, 1002, 700, True, True, False),    # transposed views: A M-contiguous (M = 1030), B K-contiguous (K = 1002)
     (3, 500, 300, 998, False, False, True),     # batched A copied per batch, broadcast B copied once
-    (2, 600, 1002, 512, False, True, False)],   # per-batch K-contiguous B
-    ids=["AK-BN", "AM-BK", "batch-bcastB", "batch-BK"])
+    (2, 600, 1002, 512, False, True, False),    # per-batch K-contiguous B
+    (0, 7, 4096, 129, False, False, False),     # skinny: padded W (N = 129) on the matrix-core GEMV
+    (0, 1, 4000, 1001, False, False, False),    # M = 1, ragged N (padded W), K whole chunks
+    (0, 20, 1003, 257, False, False, False),    # 9 <= M <= 32 with ragged K (padded x) and N (padded W)
+    (4, 5, 4100, 136, False, False, True)],     # batched x with ragged K (padded per batch), broadcast W
+    ids=["AK-BN", "AM-BK", "batch-bcastB", "batch-BK", "gemv-N129", "gemv-M1-N1001", "gemv-M20-K1003", "gemv-batch-K4100"])
 def test_misaligned_operands_padded_exact(hip, dt, batch, M, K, N, a_t, b_t, bcast):
     """An operand contiguous along one dimension whose rows are not whole 16-byte chunks is copied
-    once into zero-padded rows of whole chunks (large enough GEMMs, through the workspace), and the
-    GEMM runs on the vector loaders: A with K- or M-contiguous rows, B with N- or K-contiguous
-    rows, per batch or broadcast.  Integer-valued inputs: exact sums, half outputs rounded once,
-    int8 the low byte; fp32 exact."""
+    once into zero-padded rows of whole chunks (calls of at least 2^20 multiply-adds, through the
+    workspace), and the call runs on the vector loaders: A with K- or M-contiguous rows, B with N-
+    or K-contiguous rows, per batch or broadcast; skinny calls (M <= 32) on the matrix-core GEMV
+    where it serves the dtype (16-bit; int8 from M = 3; fp32 and int8 M = 1, 2 go to the GEMM),
+    reading chunks that straddle N or K from the zero padding.  Integer-valued inputs: exact sums,
+    half outputs rounded once, int8 the low byte; fp32 exact."""
     lead = (batch,) if batch else ()
     lo, hi = (-8, 8) if dt == INT8 else (-2, 2)
     x = ints(26, lead + (M, K), lo, hi)
