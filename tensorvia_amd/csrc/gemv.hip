@@ -659,6 +659,16 @@ static GemvPlan gemv_plan(const GemmDesc& d) {
     const int max_s = d.K / rows_min > 1 ? d.K / rows_min : 1;
     const int64_t target = d.M <= 2 ? 1376 : (d.M <= 4 ? 688 : 344);
     int s = (int)((target + strips - 1) / strips);
+    // fp32 W: slices of about 1024 rows, 2048 from 512 strips up, unless that leaves fewer than 512
+    // workgroups (a sweep of 1-16 slices over ten fp32 W shapes, K 2048-14336, N 4096-30000, M 1-8,
+    // W rotated over 4 copies: e.g. x[7, 4096] @ W[4096, 10000] 58.1 us at the workgroup target
+    // above, 48.0 at 4 slices; x[4, 2048] @ W[2048, 2048] 11.7 us at the target, 12.5 at 2).
+    if (d.dtype_a == TV_FLOAT32) {
+        const int rows = strips >= 512 ? 2048 : 1024;
+        const int s_rows = (d.K + rows - 1) / rows;
+        if (strips * s_rows >= 512) s = s_rows;
+        else if (s < s_rows) s = s_rows;
+    }
     if (s > max_s) s = max_s;
     if (s > kGemvMaxSlices) s = kGemvMaxSlices;
     if (s < min_s) s = min_s;
