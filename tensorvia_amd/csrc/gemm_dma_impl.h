@@ -1192,6 +1192,17 @@ static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int ti
     }
     int G = grid[dev];
     if (ntiles * (C::BM == 128 ? 2 : 4) > G) return 1;
+    // 16-bit 128x128 tiles above a quarter of the resident workgroups split only into segments of
+    // at least 32 k-tiles, or when the tile grid is one row or one column (each tile then streams
+    // its own rows of A or columns of B, HBM-bound, and the split adds streams).  Shorter segments
+    // of tiles whose operands are reused from L2 cost more in prologues and slot traffic than the
+    // idle CUs: bf16 [3000,4096]@[4096,1000] (192 tiles, 24 k-tiles per segment) 58.0 -> 47.3 us
+    // unsplit, [300,4096]@[4096,10000] 63.8 -> 59.2, [600,4096]@[4096,4096] 47.3 -> 43.0; but
+    // [8][3000,4096]@[4096,64] (192 tiles, one column each) 61.2 us split against 69.8,
+    // [300,4096]@[4096,4096] (96 tiles) 29.1 against 41.9, and [2048,8192]@[8192,2048] (256 tiles,
+    // 64 k-tiles per segment) 77.8 against 81.7.
+    if constexpr (!__is_same(typename C::T, int8_t) && C::BM == 128)
+        if (ntiles * 4 > G && tiles_m >= 2 && tiles_n >= 2 && ntiles * nk < 32 * (int64_t)G) return 1;
     // int8 256x256 tiles split from 16 k-tiles (K >= 2048) when they are few (at most a fifth of
     // the resident workgroups): one such tile takes a CU about 40 us at K = 4096, so a few of them
     // leave the chip idle (int8 [512,4096]@[4096,4096] 41.0 -> 33.3 us, [256,4096]@[4096,4096]
