@@ -161,6 +161,29 @@ def test_fp32_stream_k_bit_exact(hip, batch, M, K, N):
     np.testing.assert_array_equal(to_storage(plain), c)
 
 
+@pytest.mark.parametrize("batch,M,K,N,tile", [
+    (0, 2000, 300, 2050, "128x128"), (0, 300, 264, 4096, "64x128"), (0, 3000, 200, 129, "128x64"),
+    (8, 1000, 264, 129, "128x64"), (0, 3000, 4096, 129, "128x64"), (0, 300, 520, 1000, "32x128"),
+    (3, 90, 136, 500, "32x128"), (0, 300, 4096, 1000, "32x128")])
+def test_fp32_tile_choice_exact(hip, batch, M, K, N, tile):
+    """fp32 GEMMs that the tile cost rule (padded work over tile rate and CU fill) sends to each of
+    the four fp32 tiles named, with ragged M/N edges, a batch, and K = 4096 (the stream-K schedule
+    on 72 and 80 tiles).  Integer-valued inputs make every order exact: bit-exact against exact
+    sums, and equal to the plain kernel (tv_hip_gemm_noalloc: no workspace, no stream-K)."""
+    lead = (batch,) if batch else ()
+    a = ints(31, lead + (M, K), -3, 3)
+    b = ints(32, lead + (K, N), -3, 3)
+    ta, tb = to_torch(a, FLOAT32), to_torch(b, FLOAT32)
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
+    c = to_storage(hip.gemm(ta, tb))
+    np.testing.assert_array_equal(c, want)
+    plain = torch.zeros(lead + (M, N), dtype=torch.float32, device="cuda")
+    args = tv.make_args(ta, tb, plain)
+    tv.check(tv.lib().tv_hip_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(plain), c)
+
+
 def test_fp32_config1_full_size_sampled(hip):
     """c1: fp32 [2592,2048] @ [2048,4096] U[-1,1]: sampled rows/columns against fp64 sums."""
     M, K, N = 2592, 2048, 4096
@@ -286,14 +309,17 @@ def test_small_k_row_groups_exact(hip, dt, batch, M, K, N, bt):
 
 @pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, INT8])
 @pytest.mark.parametrize("batch,M,K,N", [(0, 512, 8192, 1024), (0, 300, 8192, 700), (2, 200, 8192, 520), (0, 1000, 8208, 1000),
-                                         (0, 1100, 4104, 2040), (3, 600, 4096, 1280)])
+                                         (0, 1100, 4104, 2040), (3, 600, 4096, 1280), (0, 1100, 8192, 2040),
+                                         (8, 3000, 4096, 64)])
 def test_direct_load_stream_k_bit_exact(hip, dt, batch, M, K, N):
-    """16-bit and int8 GEMMs with few, long tiles (16-bit: 32, 18, 20, 64, 144 and 150 tiles of
-    128x128, the last two in the range split only for 128x128 tiles, at most half as many tiles as
-    resident workgroups; int8: 8, 6, 6, 16, 40 and 45 of 256x256, the last two split from 33 and
-    32 k-tiles, which int8 allows for at most a fifth as many tiles as resident workgroups; K =
-    8192, 4096 and the ragged 8208 and 4104) run the direct-load kernel's stream-K schedule: tiles
-    summed in segments by several workgroups.  Integer-valued inputs: exact fp32 / int32 sums in any order, so the half
+    """16-bit and int8 GEMMs with few, long tiles (16-bit: 32, 18, 20, 64, 144, 150, 144 and 192
+    tiles of 128x128; int8: 8, 6, 6, 16, 40, 45, 40 and 96 of 256x256; K = 8192, 4096 and the
+    ragged 8208 and 4104) run the direct-load kernel's stream-K schedule: tiles summed in segments
+    by several workgroups.  16-bit 128x128 tiles split at up to half as many tiles as resident
+    workgroups, but above a quarter only into segments of at least 32 k-tiles or on a tile grid of
+    one column: 144 tiles at K = 8192 and 8 batches x 24 tiles of one column split, 144 tiles at
+    K = 4104 and 150 at K = 4096 stay whole.  int8 splits the 40 and 45 tiles from 33 and 32
+    k-tiles (at most a fifth as many tiles as resident workgroups).  Integer-valued inputs: exact fp32 / int32 sums in any order, so the half
     outputs are the exact sums rounded once, int8 the low byte, and everything equals the plain
     kernel's result (tv_hip_gemm_noalloc takes no workspace, hence no stream-K)."""
     lead = (batch,) if batch else ()
