@@ -21,8 +21,13 @@ typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
 // Used only where every wave instruction writes whole 128-byte lines (rows of a staged tile): there
 // the policy saves the L2 the output's lines (c3 bf16 epilogue -3 %, c4 -6 %); on stores that
 // cover half lines per instruction it is several times slower than a plain store.
+// A store of more than 8 bytes reads its data VGPRs after it issues: a VALU write to them needs 2
+// wait states first (gfx950; the compiler puts `s_nop 1` after its own such stores).  The compiler
+// cannot see inside the asm, and with no wait it was measured to schedule the next chunk's address
+// computation into v[0] of the data right behind the store: the store then wrote that value
+// instead of element 0, now and then.  The `s_nop 1` is part of the asm for that reason.
 __device__ inline void store_stream16(void* p, u32x4 v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1 nt" ::"v"(p), "v"(v) : "memory");
+    asm volatile("global_store_dwordx4 %0, %1, off sc1 nt\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
 }
 __device__ inline void store_stream8(void* p, uint2 v) {
     asm volatile("global_store_dwordx2 %0, %1, off sc1 nt" ::"v"(p), "v"(v) : "memory");
