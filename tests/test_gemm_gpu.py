@@ -162,13 +162,14 @@ def test_fp32_stream_k_bit_exact(hip, batch, M, K, N):
 
 
 @pytest.mark.parametrize("batch,M,K,N,tile", [
-    (0, 2000, 300, 2050, "128x128"), (0, 300, 264, 4096, "64x128"), (0, 3000, 200, 129, "128x64"),
-    (8, 1000, 264, 129, "128x64"), (0, 3000, 4096, 129, "128x64"), (0, 300, 520, 1000, "32x128"),
+    (0, 2000, 300, 2050, "128x128"), (0, 300, 264, 4096, "64x128"), (0, 4096, 200, 192, "128x64"),
+    (8, 1000, 264, 129, "128x64"), (0, 3000, 200, 129, "128x32"), (0, 3000, 4096, 129, "128x32"),
+    (0, 8192, 264, 32, "128x32"), (2, 3000, 520, 96, "128x32"), (0, 300, 520, 1000, "32x128"),
     (3, 90, 136, 500, "32x128"), (0, 300, 4096, 1000, "32x128")])
 def test_fp32_tile_choice_exact(hip, batch, M, K, N, tile):
     """fp32 GEMMs that the tile cost rule (padded work over tile rate and CU fill) sends to each of
-    the four fp32 tiles named, with ragged M/N edges, a batch, and K = 4096 (the stream-K schedule
-    on 72 and 80 tiles).  Integer-valued inputs make every order exact: bit-exact against exact
+    the five fp32 tiles named, with ragged M/N edges, batches, and K = 4096 (the stream-K schedule
+    on 120 and 80 tiles).  Integer-valued inputs make every order exact: bit-exact against exact
     sums, and equal to the plain kernel (tv_hip_gemm_noalloc: no workspace, no stream-K)."""
     lead = (batch,) if batch else ()
     a = ints(31, lead + (M, K), -3, 3)
