@@ -2,7 +2,8 @@
 // (N-contiguous).  HBM-bound: W is streamed exactly once with 16-byte buffer loads.  Two kernels:
 // a packed-dot-product kernel (gemv_kernel, no matrix cores) and a matrix-core kernel
 // (gemv_mfma_kernel) that serves 16-bit W of 64 or more columns at every M and int8 W of 128 or
-// more columns at M >= 3, where the dot products would make the VALU, not HBM, the bound.
+// more columns at M >= 3, where the dot products would make the VALU, not HBM, the bound.  A third
+// kernel (gemv_kt_kernel, below) serves 16-bit W stored K-contiguous (x @ W^T, W[N, K]) at M <= 16.
 //
 // The reference computes these shapes with mul_kernel_basic (src/backend/cpu/mul.cpp:7-25), chosen
 // because batch*M*N < 2^20 (mul.cpp:87-96), on one OpenMP thread when M = 1.
@@ -526,6 +527,153 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
 }
 
 
+// Matrix-core GEMV for K-contiguous W (W stored [N, K] row-major, used as x @ W^T: the usual
+// linear-layer layout).  The matrix core's B fragment is 8 consecutive k of one W row, so each lane
+// loads it straight from memory as one 16-byte load, with no LDS transpose:
+//  * a workgroup owns a strip of 16 x WAVES W rows and one K slice, and wave w the rows n0 + 16 w ..
+//    n0 + 16 w + 15 over the whole slice, so x's slice is staged in LDS once for all of them (x's
+//    bytes from L2 are XR / (16 WAVES) of W's);
+//  * the slice is walked in 128-k chunks, DEPTH chunks in flight per wave; per chunk a lane issues
+//    4 loads, k-steps of 32: lane l reads its row (l mod 16) at k 32q + 8 (l / 16), so each wave
+//    instruction reads 64 contiguous bytes of each of 16 rows and the 4 instructions of a chunk 256
+//    contiguous bytes of each (rows >= N and k >= the slice read zeros);
+//  * one v_mfma_f32_16x16x32 per k-step and 16-row block of x (src0 x: lane l holds x[l mod 16]
+//    [8 (l / 16) ..], row pitch padded by 16 bytes; src1 W), D[m][n] landing in lane n + 16 (m / 4),
+//    element m mod 4, which the lane stores, or publishes to slot s for the last-arriving slice to
+//    sum in slot order as in gemv_mfma_kernel.
+constexpr int kGemvKtChunk = 128;
+template <typename T, int WAVES, int DEPTH, int XR>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kt_kernel(GemvArgs g) {
+    using Acc = typename GemvTraits<T>::Acc;
+    constexpr int ES = sizeof(T), NB = 16 * WAVES, CK = kGemvKtChunk, NQ = CK / 32;
+    constexpr int MB = XR < 16 ? 1 : XR / 16;
+    static_assert(ES == 2, "16-bit W");
+    const GemmDesc& d = g.d;
+
+    extern __shared__ __attribute__((aligned(16))) char xs[]; // XR rows of kpad * ES + 16 bytes
+    __shared__ int last_flag;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lin = xcd_remap(blockIdx.x, gridDim.x);
+    const int b = lin / g.nblk;
+    const int n0 = (lin - b * g.nblk) * NB;
+    const int s = blockIdx.y;
+    const int k0 = s * g.kslice;
+    const int ks = min(d.K - k0, g.kslice); // a multiple of 8
+    const int nch = (ks + CK - 1) / CK;
+    const int kpad = nch * CK;
+    const int xpitch = kpad * ES + 16;
+    const int nsteps = (nch + DEPTH - 1) / DEPTH * DEPTH; // chunks past nch multiply zeros
+
+    const int fr = lane & 15, kg = lane >> 4;
+    const int wrow0 = n0 + 16 * wave; // this wave's first W row
+    const bool row_ok = wrow0 + fr < d.N;
+    const int64_t rowb = d.sb_n * ES;
+    const int nrows = max(1, min(16, d.N - wrow0));
+    const char* wbase = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)min(wrow0, d.N - 1) * d.sb_n + k0) * ES;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wbase, (int64_t)(nrows - 1) * rowb + (int64_t)ks * ES);
+    const unsigned lane_off = (unsigned)(fr * rowb) + (unsigned)(kg * 8 * ES);
+
+    u32x4 w[DEPTH][NQ];
+    auto issue = [&](int slot, int c) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int k = c * CK + 32 * q + 8 * kg;
+            const bool ok = row_ok && c < nch && k < ks;
+            w[slot][q] = buf_load16_nt(wr, ok ? lane_off + (unsigned)((c * CK + 32 * q) * ES) : kOOB);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) issue(j, j);
+
+    // x[b][0..XR)[k0 .. k0 + kpad) in LDS; rows >= M and columns >= ks are zero.
+    {
+        const char* xb = static_cast<const char*>(d.A) + ((int64_t)b * d.sa_b + k0) * ES;
+        const int cpr = kpad * ES / 16;
+        for (int i = tid; i < XR * cpr; i += WAVES * 64) {
+            const int m = i / cpr, c = i - m * cpr;
+            u32x4 v = u32x4{0, 0, 0, 0};
+            if (m < d.M && c * 16 < ks * ES) v = *reinterpret_cast<const u32x4*>(xb + (int64_t)m * d.sa_m * ES + c * 16);
+            *reinterpret_cast<u32x4*>(xs + m * xpitch + c * 16) = v;
+        }
+    }
+    __syncthreads();
+
+    typename Mfma<T>::Acc acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = typename Mfma<T>::Acc{0, 0, 0, 0};
+    const bool arow = XR > 8 || fr < 8;
+    const char* xa = xs + (XR > 8 ? fr : (fr & 7)) * xpitch + kg * 8 * ES; // block mb: + 16 mb rows
+    for (int c0 = 0; c0 < nsteps; c0 += DEPTH) {
+#pragma unroll
+        for (int dd = 0; dd < DEPTH; ++dd) {
+            const int c = c0 + dd;
+            const int cx = c < nch ? c : 0;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    u32x4 a = *reinterpret_cast<const u32x4*>(xa + mb * 16 * xpitch + (cx * CK + 32 * q) * ES);
+                    if (!arow || c >= nch) a = u32x4{0, 0, 0, 0};
+                    Mfma<T>::run(a, w[dd][q], acc[mb]);
+                }
+            issue(dd, c + DEPTH); // out of range past nch: zeros
+        }
+    }
+
+    // Lane (fr, kg) holds D[16 mb + 4 kg + r][wrow0 + fr], r = 0..3.
+    const int n = wrow0 + fr;
+    const size_t csz = dtype_size(d.dtype_c);
+    char* Cb = static_cast<char*>(d.C) + (int64_t)b * d.sc_b * csz;
+    if (g.nslices == 1) {
+        if (n < d.N)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = 16 * mb + 4 * kg + r;
+                    if (m < d.M) gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)n * d.sc_n, d.dtype_c, gemv_epilogue(acc[mb][r], d, b, m, n));
+                }
+        return;
+    }
+
+    // Slots [strip][S][XR][NB]: rows < M published; the last-arriving slice sums them in order.
+    const int strip = lin;
+    Acc* slots = static_cast<Acc*>(g.part) + (int64_t)strip * g.nslices * XR * NB;
+    const int col = 16 * wave + fr;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 16 * mb + 4 * kg + r;
+            if (m < d.M && m < XR)
+                __hip_atomic_store(slots + ((int64_t)s * XR + m) * NB + col, acc[mb][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    publish_and_count(g.cnt + strip, g.nslices, &last_flag);
+    if (!last_flag) return;
+    if (n < d.N)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 16 * mb + 4 * kg + r;
+                if (m < d.M && m < XR) {
+                    Acc part_v[kGemvMaxSlices];
+#pragma unroll
+                    for (int k = 0; k < kGemvMaxSlices; ++k)
+                        part_v[k] = k < g.nslices ? __hip_atomic_load(slots + ((int64_t)k * XR + m) * NB + col, __ATOMIC_RELAXED,
+                                                                      __HIP_MEMORY_SCOPE_AGENT)
+                                                  : Acc(0);
+                    Acc t = part_v[0];
+#pragma unroll
+                    for (int k = 1; k < kGemvMaxSlices; ++k)
+                        if (k < g.nslices) t += part_v[k];
+                    gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)n * d.sc_n, d.dtype_c, gemv_epilogue(t, d, b, m, n));
+                }
+            }
+    if (tid == 0) __hip_atomic_store(g.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __global__ __launch_bounds__(256) void gemv_zero_kernel(int* p, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
 }
@@ -926,8 +1074,74 @@ static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream, const GemvScr
     }
 }
 
+// The K-contiguous-W GEMV (gemv_kt_kernel): 16-bit x and W, W rows 16-byte aligned with K a
+// multiple of 8 and no padded copy, x K-contiguous with aligned rows, 1 <= M <= 16.
+static bool gemv_kt_layout_ok(const GemmDesc& d) {
+    if (d.dtype_a != d.dtype_b || (d.dtype_a != TV_BFLOAT16 && d.dtype_a != TV_FLOAT16)) return false;
+    auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (d.M < 1 || d.M > 16 || d.K < 8 || d.K % 8 || d.pad_a || d.pad_b) return false;
+    if (d.sb_k != 1 || !al(d.B) || (d.N > 1 && (d.sb_n % 8 || d.sb_n < d.K)) || (d.batch > 1 && d.sb_b % 8)) return false;
+    if (d.sa_k != 1 || !al(d.A) || (d.M > 1 && d.sa_m % 8) || (d.batch > 1 && d.sa_b % 8)) return false;
+    return true;
+}
+
+// K slices of the K-contiguous-W GEMV: about 688 workgroups in all (strips of 16 x WAVES rows x
+// slices), at least two 128-k chunks per slice, x's slice within 64 KB of LDS; at most
+// kGemvMaxSlices.
+template <typename T, int XR, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
+static int gemv_kt_run(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed) {
+    using Acc = typename GemvTraits<T>::Acc;
+    constexpr int ES = sizeof(T), NB = 16 * WAVES, CK = kGemvKtChunk;
+    constexpr int KCAP = ((kGemvXBytes / XR - 16) / ES) / CK * CK;
+    const int nblk = (d.N + NB - 1) / NB;
+    const int64_t strips = (int64_t)nblk * d.batch;
+    int S = (int)((688 + strips - 1) / strips);
+    const int max_s = d.K / (2 * CK) > 1 ? d.K / (2 * CK) : 1;
+    if (S > max_s) S = max_s;
+    const int min_s = (d.K + KCAP - 1) / KCAP;
+    if (S < min_s) S = min_s;
+    // Whole 128-k chunks per slice: a slice then starts 256-byte aligned in every W row, so each
+    // lane group's 64-byte piece is half of one 128-byte line (x[1,4096] @ W^T[4096,10000] with
+    // 824-k slices: 26.8 us, the pieces straddling lines).
+    int kslice = (d.K + S - 1) / S;
+    kslice = (kslice + CK - 1) / CK * CK;
+    if (kslice > KCAP) kslice = KCAP;
+    S = (d.K + kslice - 1) / kslice;
+    if (S > kGemvMaxSlices) return TV_E_UNSUPPORTED;
+    if ((int64_t)15 * d.sb_n * ES + (int64_t)kslice * ES >= ((int64_t)1 << 30)) return TV_E_UNSUPPORTED;
+    if (strips > 0x7FFFFFFF) return TV_E_SHAPE;
+
+    GemvArgs g;
+    g.d = d;
+    g.kslice = kslice;
+    g.nslices = S;
+    g.nblk = nblk;
+    g.cnt = nullptr;
+    g.part = nullptr;
+    if (S > 1) {
+        // A caller's fixed split buffers too small for this split: the GEMM serves the call, as it
+        // did for this layout before this kernel existed.
+        const int rc = split_buffers(stream, fixed, strips, (size_t)strips * S * XR * NB * sizeof(Acc), g);
+        if (rc) return rc == TV_E_SCRATCH ? TV_E_UNSUPPORTED : rc;
+    }
+    const int kpad = (kslice + CK - 1) / CK * CK;
+    const size_t lds = (size_t)XR * (kpad * ES + 16);
+    hipLaunchKernelGGL((gemv_kt_kernel<T, WAVES, DEPTH, XR>), dim3((unsigned)strips, S), dim3(WAVES * 64), lds, stream, g);
+    return hipGetLastError();
+}
+
+// M <= 16 (8 or 16 rows of x staged); from 17 rows the GEMM is faster (x[32,4096] @ W^T[4096,11008]:
+// 44.0 us here with 32 rows staged).
+static int launch_gemv_kt(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed) {
+    if (d.M > 16) return TV_E_UNSUPPORTED;
+    if (d.N == 0 || d.batch == 0) return 0;
+    if (d.dtype_a == TV_BFLOAT16)
+        return d.M <= 8 ? gemv_kt_run<__bf16, 8>(d, stream, fixed) : gemv_kt_run<__bf16, 16>(d, stream, fixed);
+    return d.M <= 8 ? gemv_kt_run<_Float16, 8>(d, stream, fixed) : gemv_kt_run<_Float16, 16>(d, stream, fixed);
+}
+
 int launch_gemv(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed) {
-    if (!gemv_layout_ok(d)) return TV_E_UNSUPPORTED;
+    if (!gemv_layout_ok(d)) return gemv_kt_layout_ok(d) ? launch_gemv_kt(d, stream, fixed) : TV_E_UNSUPPORTED;
     if (d.N == 0 || d.batch == 0) return 0;
     const bool mfma = (d.dtype_a == TV_BFLOAT16 || d.dtype_a == TV_FLOAT16 || (d.dtype_a == TV_INT8 && d.M >= 3)) && gemv_nl(d) == 8;
     const int64_t vec = 16 / (int64_t)dtype_size(d.dtype_a);
