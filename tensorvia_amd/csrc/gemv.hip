@@ -3,7 +3,8 @@
 // a packed-dot-product kernel (gemv_kernel, no matrix cores) and a matrix-core kernel
 // (gemv_mfma_kernel) that serves 16-bit W of 64 or more columns at every M and int8 W of 128 or
 // more columns at M >= 3, where the dot products would make the VALU, not HBM, the bound.  A third
-// kernel (gemv_kt_kernel, below) serves 16-bit W stored K-contiguous (x @ W^T, W[N, K]) at M <= 16.
+// kernel (gemv_kt_kernel, below) serves 16-bit and int8 W stored K-contiguous (x @ W^T, W[N, K]) at
+// M <= 16.
 //
 // The reference computes these shapes with mul_kernel_basic (src/backend/cpu/mul.cpp:7-25), chosen
 // because batch*M*N < 2^20 (mul.cpp:87-96), on one OpenMP thread when M = 1.
@@ -533,21 +534,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
 //  * a workgroup owns a strip of 16 x WAVES W rows and one K slice, and wave w the rows n0 + 16 w ..
 //    n0 + 16 w + 15 over the whole slice, so x's slice is staged in LDS once for all of them (x's
 //    bytes from L2 are XR / (16 WAVES) of W's);
-//  * the slice is walked in 128-k chunks, DEPTH chunks in flight per wave; per chunk a lane issues
-//    4 loads, k-steps of 32: lane l reads its row (l mod 16) at k 32q + 8 (l / 16), so each wave
-//    instruction reads 64 contiguous bytes of each of 16 rows and the 4 instructions of a chunk 256
-//    contiguous bytes of each (rows >= N and k >= the slice read zeros);
-//  * one v_mfma_f32_16x16x32 per k-step and 16-row block of x (src0 x: lane l holds x[l mod 16]
-//    [8 (l / 16) ..], row pitch padded by 16 bytes; src1 W), D[m][n] landing in lane n + 16 (m / 4),
-//    element m mod 4, which the lane stores, or publishes to slot s for the last-arriving slice to
-//    sum in slot order as in gemv_mfma_kernel.
-constexpr int kGemvKtChunk = 128;
+//  * the slice is walked in 256-byte chunks of each row (128 k at 16 bits, 256 in int8), DEPTH
+//    chunks in flight per wave; per chunk a lane issues 4 loads, k-steps of 4 VEC (VEC = 16 bytes
+//    of k): lane l reads its row (l mod 16) at k 4 VEC q + VEC (l / 16), so each wave instruction
+//    reads 64 contiguous bytes of each of 16 rows and the 4 instructions of a chunk 256 contiguous
+//    bytes of each (rows >= N and k >= the slice read zeros);
+//  * one v_mfma_f32_16x16x32 (int8: v_mfma_i32_16x16x64_i8, exact int32 sums) per k-step and
+//    16-row block of x (src0 x: lane l holds x[l mod 16][VEC (l / 16) ..], row pitch padded by 16
+//    bytes; src1 W), D[m][n] landing in lane n + 16 (m / 4), element m mod 4, which the lane
+//    stores, or publishes to slot s for the last-arriving slice to sum in slot order as in
+//    gemv_mfma_kernel.
+template <typename T> constexpr int gemv_kt_chunk() { return 256 / (int)sizeof(T); }
 template <typename T, int WAVES, int DEPTH, int XR>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kt_kernel(GemvArgs g) {
     using Acc = typename GemvTraits<T>::Acc;
-    constexpr int ES = sizeof(T), NB = 16 * WAVES, CK = kGemvKtChunk, NQ = CK / 32;
+    constexpr int ES = sizeof(T), VEC = 16 / ES, KSTEP = 4 * VEC, NB = 16 * WAVES, CK = gemv_kt_chunk<T>(), NQ = CK / KSTEP;
     constexpr int MB = XR < 16 ? 1 : XR / 16;
-    static_assert(ES == 2, "16-bit W");
+    static_assert(ES == 1 || ES == 2, "16-bit or 8-bit W");
     const GemmDesc& d = g.d;
 
     extern __shared__ __attribute__((aligned(16))) char xs[]; // XR rows of kpad * ES + 16 bytes
@@ -559,7 +562,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kt_kernel(GemvArgs g) {
     const int n0 = (lin - b * g.nblk) * NB;
     const int s = blockIdx.y;
     const int k0 = s * g.kslice;
-    const int ks = min(d.K - k0, g.kslice); // a multiple of 8
+    const int ks = min(d.K - k0, g.kslice); // a multiple of VEC
     const int nch = (ks + CK - 1) / CK;
     const int kpad = nch * CK;
     const int xpitch = kpad * ES + 16;
@@ -572,15 +575,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kt_kernel(GemvArgs g) {
     const int nrows = max(1, min(16, d.N - wrow0));
     const char* wbase = static_cast<const char*>(d.B) + ((int64_t)b * d.sb_b + (int64_t)min(wrow0, d.N - 1) * d.sb_n + k0) * ES;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wbase, (int64_t)(nrows - 1) * rowb + (int64_t)ks * ES);
-    const unsigned lane_off = (unsigned)(fr * rowb) + (unsigned)(kg * 8 * ES);
+    const unsigned lane_off = (unsigned)(fr * rowb) + (unsigned)(kg * 16);
 
     u32x4 w[DEPTH][NQ];
     auto issue = [&](int slot, int c) {
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-            const int k = c * CK + 32 * q + 8 * kg;
+            const int k = c * CK + KSTEP * q + VEC * kg;
             const bool ok = row_ok && c < nch && k < ks;
-            w[slot][q] = buf_load16_nt(wr, ok ? lane_off + (unsigned)((c * CK + 32 * q) * ES) : kOOB);
+            w[slot][q] = buf_load16_nt(wr, ok ? lane_off + (unsigned)((c * CK + KSTEP * q) * ES) : kOOB);
         }
     };
 #pragma unroll
@@ -603,7 +606,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kt_kernel(GemvArgs g) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = typename Mfma<T>::Acc{0, 0, 0, 0};
     const bool arow = XR > 8 || fr < 8;
-    const char* xa = xs + (XR > 8 ? fr : (fr & 7)) * xpitch + kg * 8 * ES; // block mb: + 16 mb rows
+    const char* xa = xs + (XR > 8 ? fr : (fr & 7)) * xpitch + kg * 16; // block mb: + 16 mb rows
     for (int c0 = 0; c0 < nsteps; c0 += DEPTH) {
 #pragma unroll
         for (int dd = 0; dd < DEPTH; ++dd) {
@@ -613,7 +616,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kt_kernel(GemvArgs g) {
             for (int q = 0; q < NQ; ++q)
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) {
-                    u32x4 a = *reinterpret_cast<const u32x4*>(xa + mb * 16 * xpitch + (cx * CK + 32 * q) * ES);
+                    u32x4 a = *reinterpret_cast<const u32x4*>(xa + mb * 16 * xpitch + (cx * CK + KSTEP * q) * ES);
                     if (!arow || c >= nch) a = u32x4{0, 0, 0, 0};
                     Mfma<T>::run(a, w[dd][q], acc[mb]);
                 }
@@ -1074,24 +1077,25 @@ static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream, const GemvScr
     }
 }
 
-// The K-contiguous-W GEMV (gemv_kt_kernel): 16-bit x and W, W rows 16-byte aligned with K a
-// multiple of 8 and no padded copy, x K-contiguous with aligned rows, 1 <= M <= 16.
+// The K-contiguous-W GEMV (gemv_kt_kernel): 16-bit or int8 x and W, W rows 16-byte aligned with K
+// a multiple of the 16-byte vector and no padded copy, x K-contiguous with aligned rows, 1 <= M <= 16.
 static bool gemv_kt_layout_ok(const GemmDesc& d) {
-    if (d.dtype_a != d.dtype_b || (d.dtype_a != TV_BFLOAT16 && d.dtype_a != TV_FLOAT16)) return false;
+    if (d.dtype_a != d.dtype_b || (d.dtype_a != TV_BFLOAT16 && d.dtype_a != TV_FLOAT16 && d.dtype_a != TV_INT8)) return false;
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-    if (d.M < 1 || d.M > 16 || d.K < 8 || d.K % 8 || d.pad_a || d.pad_b) return false;
-    if (d.sb_k != 1 || !al(d.B) || (d.N > 1 && (d.sb_n % 8 || d.sb_n < d.K)) || (d.batch > 1 && d.sb_b % 8)) return false;
-    if (d.sa_k != 1 || !al(d.A) || (d.M > 1 && d.sa_m % 8) || (d.batch > 1 && d.sa_b % 8)) return false;
+    const int64_t v = 16 / (int64_t)dtype_size(d.dtype_a);
+    if (d.M < 1 || d.M > 16 || d.K < v || d.K % v || d.pad_a || d.pad_b) return false;
+    if (d.sb_k != 1 || !al(d.B) || (d.N > 1 && (d.sb_n % v || d.sb_n < d.K)) || (d.batch > 1 && d.sb_b % v)) return false;
+    if (d.sa_k != 1 || !al(d.A) || (d.M > 1 && d.sa_m % v) || (d.batch > 1 && d.sa_b % v)) return false;
     return true;
 }
 
 // K slices of the K-contiguous-W GEMV: about 688 workgroups in all (strips of 16 x WAVES rows x
-// slices), at least two 128-k chunks per slice, x's slice within 64 KB of LDS; at most
+// slices), at least two 256-byte chunks per slice, x's slice within 64 KB of LDS; at most
 // kGemvMaxSlices.
 template <typename T, int XR, int WAVES = kGemvMfmaWaves, int DEPTH = gemv_mfma_depth<T>()>
 static int gemv_kt_run(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed) {
     using Acc = typename GemvTraits<T>::Acc;
-    constexpr int ES = sizeof(T), NB = 16 * WAVES, CK = kGemvKtChunk;
+    constexpr int ES = sizeof(T), NB = 16 * WAVES, CK = gemv_kt_chunk<T>();
     constexpr int KCAP = ((kGemvXBytes / XR - 16) / ES) / CK * CK;
     const int nblk = (d.N + NB - 1) / NB;
     const int64_t strips = (int64_t)nblk * d.batch;
@@ -1100,7 +1104,7 @@ static int gemv_kt_run(const GemmDesc& d, hipStream_t stream, const GemvScratch*
     if (S > max_s) S = max_s;
     const int min_s = (d.K + KCAP - 1) / KCAP;
     if (S < min_s) S = min_s;
-    // Whole 128-k chunks per slice: a slice then starts 256-byte aligned in every W row, so each
+    // Whole 256-byte chunks per slice: a slice then starts 256-byte aligned in every W row, so each
     // lane group's 64-byte piece is half of one 128-byte line (x[1,4096] @ W^T[4096,10000] with
     // 824-k slices: 26.8 us, the pieces straddling lines).
     int kslice = (d.K + S - 1) / S;
@@ -1137,6 +1141,8 @@ static int launch_gemv_kt(const GemmDesc& d, hipStream_t stream, const GemvScrat
     if (d.N == 0 || d.batch == 0) return 0;
     if (d.dtype_a == TV_BFLOAT16)
         return d.M <= 8 ? gemv_kt_run<__bf16, 8>(d, stream, fixed) : gemv_kt_run<__bf16, 16>(d, stream, fixed);
+    if (d.dtype_a == TV_INT8)
+        return d.M <= 8 ? gemv_kt_run<int8_t, 8>(d, stream, fixed) : gemv_kt_run<int8_t, 16>(d, stream, fixed);
     return d.M <= 8 ? gemv_kt_run<_Float16, 8>(d, stream, fixed) : gemv_kt_run<_Float16, 16>(d, stream, fixed);
 }
 

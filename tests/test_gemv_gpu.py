@@ -80,29 +80,40 @@ def test_skinny_m_matrix_core_exact(hip, dt, M, KN):
     np.testing.assert_array_equal(c, half_bits(np.matmul(x, w), dt))
 
 
-@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16])
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, INT8])
 @pytest.mark.parametrize("M", [1, 3, 8, 9, 16, 17, 32])
 @pytest.mark.parametrize("batch,K,N,bcast", [(0, 4096, 11008, False), (0, 4096, 1000, False), (0, 8200, 130, False),
-                                             (0, 136, 4104, False), (3, 1032, 520, True), (2, 4096, 2000, False)],
-                         ids=["K4096-N11008", "K4096-N1000", "K8200-N130", "K136-N4104", "b3-bcast", "b2"])
+                                             (0, 8208, 130, False), (0, 136, 4104, False), (0, 144, 4104, False),
+                                             (3, 1032, 520, True), (2, 4096, 2000, False)],
+                         ids=["K4096-N11008", "K4096-N1000", "K8200-N130", "K8208-N130", "K136-N4104", "K144-N4104",
+                              "b3-bcast", "b2"])
 def test_k_contiguous_w_matrix_core_exact(hip, dt, M, batch, K, N, bcast):
     """x @ W^T with W stored [N, K] (K-contiguous, the linear-layer layout): M <= 16 on the
     matrix-core GEMV that loads W's fragments directly (gemv_kt_kernel: 64-row strips, K split into
-    slices of whole 128-k chunks or not, K = 136 one partial chunk, ragged N, 8 or 16 staged rows
-    of x, batches with one W or per-batch W), M = 17 and 32 on the GEMM.  Integer-valued inputs:
-    exact sums, so the half outputs are the exact sums rounded once; equal to the no-allocation
-    entry point."""
+    slices of whole 256-byte chunks or not, K = 8208 and 144 ending in a partial chunk, ragged N, 8
+    or 16 staged rows of x, batches with one W or per-batch W; K not a multiple of the 16-byte
+    vector, and M = 17 and 32, on the GEMM).  Integer-valued inputs: exact sums, so the half
+    outputs are the exact sums rounded once, int8 the low byte and int32 the sums; equal to the
+    no-allocation entry point."""
     import ctypes
     import tensorvia_amd as tv
     lead = (batch,) if batch else ()
-    x = rng.uniform_int(50 + M, int(np.prod(lead + (M, K))), -2, 2).astype(np.float32).reshape(lead + (M, K))
     wshape = (N, K) if (bcast or not batch) else lead + (N, K)
-    w = rng.uniform_int(51, int(np.prod(wshape)), -2, 2).astype(np.float32).reshape(wshape)
-    tx, tw = to_torch(half_bits(x, dt), dt), to_torch(half_bits(w, dt), dt)
-    wt = tw.transpose(-1, -2)
-    exact = np.matmul(x.astype(np.float64), np.swapaxes(w, -1, -2).astype(np.float64)).astype(np.float32)
-    c = to_storage(hip.gemm(tx, wt))
-    np.testing.assert_array_equal(c, half_bits(exact, dt))
+    lo, hi = (-128, 127) if dt == INT8 else (-2, 2)
+    x = rng.uniform_int(50 + M, int(np.prod(lead + (M, K))), lo, hi).astype(np.float32).reshape(lead + (M, K))
+    w = rng.uniform_int(51, int(np.prod(wshape)), lo, hi).astype(np.float32).reshape(wshape)
+    exact = np.matmul(x.astype(np.int64), np.swapaxes(w, -1, -2).astype(np.int64))
+    if dt == INT8:
+        tx, tw = to_torch(x.astype(np.int8), INT8), to_torch(w.astype(np.int8), INT8)
+        wt = tw.transpose(-1, -2)
+        c = to_storage(hip.gemm(tx, wt))
+        np.testing.assert_array_equal(c, exact.astype(np.int8))
+        np.testing.assert_array_equal(to_storage(hip.gemm(tx, wt, out_dtype=INT32)), exact.astype(np.int32))
+    else:
+        tx, tw = to_torch(half_bits(x, dt), dt), to_torch(half_bits(w, dt), dt)
+        wt = tw.transpose(-1, -2)
+        c = to_storage(hip.gemm(tx, wt))
+        np.testing.assert_array_equal(c, half_bits(exact.astype(np.float32), dt))
     plain = torch.zeros(lead + (M, N), dtype=tx.dtype, device="cuda")
     args = tv.make_args(tx, wt, plain)
     tv.check(tv.lib().tv_hip_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
