@@ -143,9 +143,12 @@ int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_st
  * different streams, or from different threads) race and must be serialised by the caller. */
 int tv_hip_gemm_noalloc(const tv_gemm_args* args, void* hip_stream);
 
-/* Skinny-M (M <= 8) matrix-vector path, HBM-streaming: matrix cores for bf16/fp16 W of 64 or more
- * columns and int8 W of 128 or more columns at M >= 3, packed dot products otherwise.  Returns TV_E_UNSUPPORTED for M > 8 or for a dtype pair
- * or layout it does not serve. */
+/* Skinny-M (M <= 8) matrix-vector path, HBM-streaming.  W N-contiguous (x @ W, W[K, N] row-major):
+ * matrix cores for bf16/fp16 W of 64 or more columns and int8 W of 128 or more columns at M >= 3,
+ * packed dot products otherwise.  W K-contiguous (x @ W^T, W[N, K] row-major, K a multiple of the
+ * 16-byte vector, rows 16-byte aligned): matrix cores for bf16, fp16 and int8.  Returns
+ * TV_E_UNSUPPORTED for M > 8 or for a dtype pair or layout it does not serve (tv_hip_gemm serves
+ * every layout). */
 int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream);
 
 /* Strided -> contiguous copy of one tensor view on the device (ndim <= TV_MAX_DIMS).  Element

@@ -3,8 +3,8 @@
 // a packed-dot-product kernel (gemv_kernel, no matrix cores) and a matrix-core kernel
 // (gemv_mfma_kernel) that serves 16-bit W of 64 or more columns at every M and int8 W of 128 or
 // more columns at M >= 3, where the dot products would make the VALU, not HBM, the bound.  A third
-// kernel (gemv_kt_kernel, below) serves 16-bit and int8 W stored K-contiguous (x @ W^T, W[N, K]) at
-// M <= 16.
+// kernel (gemv_kt_kernel, below) serves 16-bit and int8 W stored K-contiguous (x @ W^T, W[N, K])
+// at M <= 16.
 //
 // The reference computes these shapes with mul_kernel_basic (src/backend/cpu/mul.cpp:7-25), chosen
 // because batch*M*N < 2^20 (mul.cpp:87-96), on one OpenMP thread when M = 1.
@@ -539,9 +539,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
 //    of k): lane l reads its row (l mod 16) at k 4 VEC q + VEC (l / 16), so each wave instruction
 //    reads 64 contiguous bytes of each of 16 rows and the 4 instructions of a chunk 256 contiguous
 //    bytes of each (rows >= N and k >= the slice read zeros);
-//  * one v_mfma_f32_16x16x32 (int8: v_mfma_i32_16x16x64_i8, exact int32 sums) per k-step and
-//    16-row block of x (src0 x: lane l holds x[l mod 16][VEC (l / 16) ..], row pitch padded by 16
-//    bytes; src1 W), D[m][n] landing in lane n + 16 (m / 4), element m mod 4, which the lane
+//  * one v_mfma_f32_16x16x32 (int8: v_mfma_i32_16x16x64_i8, exact int32 sums) per k-step and 16-row block of x (src0 x: lane l holds x[l mod 16][VEC (l / 16)
+//    ..], row pitch padded by 16 bytes; src1 W), D[m][n] landing in lane n + 16 (m / 4), element m mod 4, which the lane
 //    stores, or publishes to slot s for the last-arriving slice to sum in slot order as in
 //    gemv_mfma_kernel.
 template <typename T> constexpr int gemv_kt_chunk() { return 256 / (int)sizeof(T); }
@@ -550,7 +549,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kt_kernel(GemvArgs g) {
     using Acc = typename GemvTraits<T>::Acc;
     constexpr int ES = sizeof(T), VEC = 16 / ES, KSTEP = 4 * VEC, NB = 16 * WAVES, CK = gemv_kt_chunk<T>(), NQ = CK / KSTEP;
     constexpr int MB = XR < 16 ? 1 : XR / 16;
-    static_assert(ES == 1 || ES == 2, "16-bit or 8-bit W");
+    static_assert(ES == 1 || ES == 2, "8- or 16-bit W");
     const GemmDesc& d = g.d;
 
     extern __shared__ __attribute__((aligned(16))) char xs[]; // XR rows of kpad * ES + 16 bytes
@@ -1080,7 +1079,10 @@ static int launch_gemv_mfma(const GemmDesc& d, hipStream_t stream, const GemvScr
 // The K-contiguous-W GEMV (gemv_kt_kernel): 16-bit or int8 x and W, W rows 16-byte aligned with K
 // a multiple of the 16-byte vector and no padded copy, x K-contiguous with aligned rows, 1 <= M <= 16.
 static bool gemv_kt_layout_ok(const GemmDesc& d) {
-    if (d.dtype_a != d.dtype_b || (d.dtype_a != TV_BFLOAT16 && d.dtype_a != TV_FLOAT16 && d.dtype_a != TV_INT8)) return false;
+    if (d.dtype_a != d.dtype_b) return false;
+    // fp32 W stays on the GEMM: through this kernel (four v_mfma_f32_16x16x4f32 per 16 bytes) it
+    // measured slower at large N (x[8,4096] @ W^T[4096,32000] 129.4 us against 105.3).
+    if (d.dtype_a != TV_BFLOAT16 && d.dtype_a != TV_FLOAT16 && d.dtype_a != TV_INT8) return false;
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     const int64_t v = 16 / (int64_t)dtype_size(d.dtype_a);
     if (d.M < 1 || d.M > 16 || d.K < v || d.K % v || d.pad_a || d.pad_b) return false;

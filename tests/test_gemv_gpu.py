@@ -80,7 +80,7 @@ def test_skinny_m_matrix_core_exact(hip, dt, M, KN):
     np.testing.assert_array_equal(c, half_bits(np.matmul(x, w), dt))
 
 
-@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, INT8])
+@pytest.mark.parametrize("dt", [BFLOAT16, FLOAT16, INT8, FLOAT32])
 @pytest.mark.parametrize("M", [1, 3, 8, 9, 16, 17, 32])
 @pytest.mark.parametrize("batch,K,N,bcast", [(0, 4096, 11008, False), (0, 4096, 1000, False), (0, 8200, 130, False),
                                              (0, 8208, 130, False), (0, 136, 4104, False), (0, 144, 4104, False),
@@ -92,9 +92,9 @@ def test_k_contiguous_w_matrix_core_exact(hip, dt, M, batch, K, N, bcast):
     matrix-core GEMV that loads W's fragments directly (gemv_kt_kernel: 64-row strips, K split into
     slices of whole 256-byte chunks or not, K = 8208 and 144 ending in a partial chunk, ragged N, 8
     or 16 staged rows of x, batches with one W or per-batch W; K not a multiple of the 16-byte
-    vector, and M = 17 and 32, on the GEMM).  Integer-valued inputs: exact sums, so the half
-    outputs are the exact sums rounded once, int8 the low byte and int32 the sums; equal to the
-    no-allocation entry point."""
+    vector, fp32, and M = 17 and 32, on the GEMM).  Integer-valued inputs: exact sums, so the half
+    outputs are the exact sums rounded once, int8 the low byte, int32 and fp32 the sums; equal to
+    the no-allocation entry point."""
     import ctypes
     import tensorvia_amd as tv
     lead = (batch,) if batch else ()
@@ -109,6 +109,11 @@ def test_k_contiguous_w_matrix_core_exact(hip, dt, M, batch, K, N, bcast):
         c = to_storage(hip.gemm(tx, wt))
         np.testing.assert_array_equal(c, exact.astype(np.int8))
         np.testing.assert_array_equal(to_storage(hip.gemm(tx, wt, out_dtype=INT32)), exact.astype(np.int32))
+    elif dt == FLOAT32:
+        tx, tw = to_torch(x, FLOAT32), to_torch(w, FLOAT32)
+        wt = tw.transpose(-1, -2)
+        c = to_storage(hip.gemm(tx, wt))
+        np.testing.assert_array_equal(c, exact.astype(np.float32))
     else:
         tx, tw = to_torch(half_bits(x, dt), dt), to_torch(half_bits(w, dt), dt)
         wt = tw.transpose(-1, -2)
@@ -187,11 +192,24 @@ def test_gemv_unsupported_layouts_report_and_gemm_serves_them(hip):
     K, N = 256, 64
     x = rng.uniform_int(44, K, -2, 2).astype(np.float32).reshape(1, K)
     w = rng.uniform_int(45, K * N, -2, 2).astype(np.float32).reshape(K, N)
-    wt = to_torch(np.ascontiguousarray(w.T), FLOAT32).t()  # K-contiguous W
+    # K-contiguous W (x @ W^T with W stored [N, K]) is served by tv_hip_gemv itself at 16 bits ...
+    wt16 = to_torch(half_bits(np.ascontiguousarray(w.T), BFLOAT16), BFLOAT16).t()
+    c16 = hip.gemv(to_torch(half_bits(x, BFLOAT16), BFLOAT16), wt16, out_dtype=FLOAT32)
+    np.testing.assert_array_equal(to_storage(c16), orc.mul(x, FLOAT32, w, FLOAT32))
+    # ... but not in fp32 (the GEMM serves it), nor W contiguous along neither dimension (every
+    # other column of a [K, 2N] array)
+    wt = to_torch(np.ascontiguousarray(w.T), FLOAT32).t()
     with pytest.raises(hip.TensorviaHipError) as e:
         hip.gemv(to_torch(x, FLOAT32), wt)
     assert e.value.code == hip.TV_E_UNSUPPORTED
-    c = to_storage(hip.gemm(to_torch(x, FLOAT32), wt))
+    np.testing.assert_array_equal(to_storage(hip.gemm(to_torch(x, FLOAT32), wt)), orc.mul(x, FLOAT32, w, FLOAT32))
+    w2 = np.zeros((K, 2 * N), np.float32)
+    w2[:, ::2] = w
+    wg = to_torch(w2, FLOAT32)[:, ::2]
+    with pytest.raises(hip.TensorviaHipError) as e:
+        hip.gemv(to_torch(x, FLOAT32), wg)
+    assert e.value.code == hip.TV_E_UNSUPPORTED
+    c = to_storage(hip.gemm(to_torch(x, FLOAT32), wg))
     np.testing.assert_array_equal(c, orc.mul(x, FLOAT32, w, FLOAT32))
     with pytest.raises(hip.TensorviaHipError):
         hip.gemv(to_torch(np.zeros((9, K), np.float32), FLOAT32), to_torch(w, FLOAT32))
