@@ -6,6 +6,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <condition_variable>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <thread>
@@ -53,6 +54,11 @@ class HIPContext : public ContextImpl {
     std::unique_ptr<Staging> m_staging;
     std::mutex m_staging_mu;
     Staging& staging();
+    // Device blocks of released tensors, by capacity (see alloc()).
+    std::multimap<size_t, void*> m_free;
+    size_t m_cached = 0;
+    size_t m_cache_limit = 0;
+    mutable std::mutex m_cache_mu;
 
 public:
     HIPContext();
@@ -68,14 +74,34 @@ public:
     void copy_d2h(void* dst, const void* src, size_t bytes);
     // The process-wide context, created on first use (no GPU is touched at library load).
     static std::shared_ptr<HIPContext> get();
+
+    // Device memory of this context's tensors.  A released block is kept and handed to the next
+    // tensor of about its size, so an op that returns a new tensor (ops::Mul's result) costs no
+    // hipMalloc / hipFree once the sizes repeat; the reference's CUDA backend allocates every result
+    // with cudaMalloc and frees it with cudaFree (src/backend/cuda/mul.cu:64,
+    // include/backend/cuda/cuda_tensor.cpp:14-30).  All work of the context is on its one stream,
+    // so a block released after its last use was enqueued there can serve later work on that
+    // stream without a synchronisation.  Requests are rounded up (512 bytes below 1 MiB, 2 MiB
+    // above) and served from a cached block at most a quarter larger.  Cached bytes are capped
+    // (TV_HIP_CACHE_LIMIT_MB, default a quarter of the device's memory; 0 turns the cache off):
+    // past the cap a released block is freed after a stream synchronisation, as without a cache.
+    // When hipMalloc fails the cache is emptied and the allocation tried once more.
+    // alloc() returns nullptr for 0 bytes and sets *capacity to the block's size.
+    void* alloc(size_t bytes, size_t* capacity);
+    void release(void* p, size_t capacity);
+    void empty_cache();
+    size_t cached_bytes() const;
+    size_t cache_limit() const { return m_cache_limit; }
 };
 
-// hipMalloc-backed storage (reference CUDATensor, include/backend/cuda/cuda_tensor.cpp:14-70).
+// Device storage from the context's block cache (reference CUDATensor,
+// include/backend/cuda/cuda_tensor.cpp:14-70, which calls cudaMalloc / cudaFree directly).
 class HIPTensor : public TensorImpl {
     size_t m_numel = 0;
     via::DataType m_dtype = via::DataType::FLOAT32;
     std::shared_ptr<HIPContext> m_context;
     void* m_data = nullptr;
+    size_t m_capacity = 0; // bytes of the context block holding the data
 
 public:
     HIPTensor(void* host_ptr, size_t numel, via::DataType dtype, std::shared_ptr<HIPContext> ctx);
@@ -119,6 +145,9 @@ template <via::Device D> struct MulImpl;
 template <> struct MulImpl<via::Device::HIP> {
     static Tensor execute(const Tensor& a, const Tensor& b);
 };
+// As the reference declares its backends' plugins (include/backend/cpu/ops/mul.h:15,
+// include/backend/cuda/ops/mul.h:15): the definition lives in libtensorvia.so.
+extern template struct MulImpl<via::Device::HIP>;
 
 template <via::Device D> struct MulBiasActImpl;
 // The fused matmul + bias + activation (tv_hip_gemm_ex).

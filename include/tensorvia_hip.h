@@ -49,7 +49,9 @@
  * partial sums, and large GEMMs their zero-padded copies of operands whose rows are not whole
  * 16-byte chunks, in a workspace per (device, stream): calls on one stream are ordered by that
  * stream, and calls on different streams use different workspaces, so concurrent streams are safe.
- * Growing a stream's workspace synchronises that stream once.
+ * Growing a stream's workspace synchronises that stream once.  When the workspace cannot be
+ * allocated (device memory exhausted), the call runs on kernels that need none (the unsplit GEMM,
+ * the element-gather loader), more slowly, and still returns 0.
  */
 #ifndef TENSORVIA_HIP_H
 #define TENSORVIA_HIP_H
@@ -133,8 +135,11 @@ int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_st
  * counters per GPU, held until the process ends, instead of tv_hip_gemm's workspace.  GEMMs
  * (M > 8) that tv_hip_gemm splits with its stream-K schedule, whose partial tiles need a
  * workspace, run unsplit here, so their fp32 and 16-bit results can differ from tv_hip_gemm's in
- * the last bits (summation order); every other call, and every int8 call, gives tv_hip_gemm's
- * results bit for bit.  A call whose split needs more returns TV_E_SCRATCH at M <= 8 (e.g. M = 8
+ * the last bits (summation order).  So can float calls with an operand whose rows are not whole
+ * 16-byte chunks (e.g. bf16 W[4096,129]): tv_hip_gemm copies such an operand into padded rows (a
+ * skinny call then runs on the matrix-core GEMV), while this entry point reads it in place with
+ * the GEMM's element-gather loader, which sums K in another order.  Every other call, and every
+ * int8 call, gives tv_hip_gemm's results bit for bit.  A call whose split needs more returns TV_E_SCRATCH at M <= 8 (e.g. M = 8
  * bf16 needs 2 KiB per (64-column strip, K-slice) pair: c5's x[8,4096] @ W[4096,11008] needs
  * 1.4 MiB); at 9 <= M <= 32 it runs the GEMM instead (e.g. M = 32 bf16 on c5's W needs 11 MiB of
  * partials), whose fp32 and 16-bit results can then differ from tv_hip_gemm's in the last bits.
@@ -195,7 +200,13 @@ int tv_hip_abi_version(void);
  * the device.  Lets host code prove error propagation without a GPU.  count = 0 disarms. */
 void tv_hip_inject_fault(int code, int count);
 
-#define TV_HIP_ABI_VERSION 5
+/* Test hook: the next `count` requests for the library's per-stream workspace (split-K slots,
+ * padded operand copies) allocate, asking the HIP runtime for more memory than any device has, so
+ * they fail as they would when device memory is exhausted, and the calls take their no-workspace
+ * paths.  count = 0 disarms. */
+void tv_hip_inject_alloc_failure(int count);
+
+#define TV_HIP_ABI_VERSION 6
 
 #ifdef __cplusplus
 }

@@ -28,7 +28,8 @@ TV_E_NULL, TV_E_SHAPE, TV_E_DTYPE, TV_E_UNSUPPORTED, TV_E_INJECTED, TV_E_NOMEM, 
 
 # Every symbol include/tensorvia_hip.h declares.
 EXPORTED_SYMBOLS = ("tv_hip_gemm", "tv_hip_gemm_ex", "tv_hip_gemm_noalloc", "tv_hip_gemv", "tv_hip_repack", "tv_hip_typecast", "tv_hip_fill",
-                    "tv_hip_random", "tv_hip_strerror", "tv_hip_abi_version", "tv_hip_inject_fault")
+                    "tv_hip_random", "tv_hip_strerror", "tv_hip_abi_version", "tv_hip_inject_fault",
+                    "tv_hip_inject_alloc_failure")
 
 
 class TvGemmArgs(ctypes.Structure):
@@ -106,6 +107,8 @@ def lib() -> ctypes.CDLL:
         L.tv_hip_abi_version.restype = ctypes.c_int
         L.tv_hip_inject_fault.argtypes = [ctypes.c_int, ctypes.c_int]
         L.tv_hip_inject_fault.restype = None
+        L.tv_hip_inject_alloc_failure.argtypes = [ctypes.c_int]
+        L.tv_hip_inject_alloc_failure.restype = None
         _lib = L
     return _lib
 

@@ -99,7 +99,8 @@ int run_gemm(const tv_gemm_args* args, const tvk::GemmDesc& d0, hipStream_t s, c
         // the caller's fixed split-K buffers are too small above M = 8, the GEMM serves it.
         if (d.M <= 32) {
             const int rc = tvk::launch_gemv(d, s, fixed);
-            if (rc != TV_E_UNSUPPORTED && !(rc == TV_E_SCRATCH && d.M > 8)) return rc;
+            // No room for the split-K slots (TV_E_NOMEM): the GEMM needs none in its plain form.
+            if (rc != TV_E_UNSUPPORTED && rc != TV_E_NOMEM && !(rc == TV_E_SCRATCH && d.M > 8)) return rc;
         }
         return tvk::launch_gemm_mfma(d, s, fixed == nullptr);
     }
@@ -116,6 +117,8 @@ void tv_hip_inject_fault(int code, int count) {
     g_fault_code.store(code);
     g_fault_count.store(count < 0 ? 0 : count);
 }
+
+void tv_hip_inject_alloc_failure(int count) { tvk::inject_alloc_failure(count); }
 
 int tv_hip_gemm(const tv_gemm_args* args, void* hip_stream) {
     int code;

@@ -1142,23 +1142,24 @@ void gemm_dma_chain_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, in
     wait_vmcnt<0>();
 }
 
+// Workgroups of `kernel` (THREADS threads, static LDS only) resident at once on device dev: the
+// occupancy API's count per CU times the CUs; 0 if the runtime cannot tell.
+static int resident_grid(const void* kernel, int threads, int dev) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
+        return 0;
+    return per_cu * cus;
+}
+
 // Chained launch: one workgroup per CU walking several tiles.  Returns 1 if it did not launch:
 // fewer than two tiles per CU, or an output other than 16-bit with 16-byte aligned rows.
 template <class C>
 static int run_dma_chain(const GemmDesc& d, hipStream_t stream, int group_m, int tiles_m, int tiles_n, int64_t ntiles, int c_vec) {
     if (c_vec != 2 || !(d.dtype_c == TV_BFLOAT16 || d.dtype_c == TV_FLOAT16)) return 1;
-    static int grid[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
-    if (grid[dev] <= 0) {
-        int per_cu = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(gemm_dma_chain_kernel<C>), C::THREADS, 0) !=
-                hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
-            return 1;
-        grid[dev] = per_cu * cus;
-    }
-    const int G = grid[dev];
+    static std::atomic<int> grid[kMaxDevices];
+    const int G = cached_per_device(grid, [](int dev) { return resident_grid(reinterpret_cast<const void*>(gemm_dma_chain_kernel<C>), C::THREADS, dev); });
+    if (G <= 0) return 1;
     if (ntiles < 2 * (int64_t)G) return 1;
     hipLaunchKernelGGL(gemm_dma_chain_kernel<C>, dim3((unsigned)G), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n, group_m, (int)ntiles);
     return hipGetLastError();
@@ -1179,18 +1180,9 @@ template <class C, bool FUSED>
 static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int tiles_m, int tiles_n, int64_t ntiles, int c_vec) {
     const int nk = (d.K + C::BK - 1) / C::BK;
     if (nk < (__is_same(typename C::T, int8_t) ? 16 : 64)) return 1;
-    static int grid[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
-    if (grid[dev] <= 0) {
-        int per_cu = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(gemm_dma_sk_kernel<C, false>), C::THREADS,
-                                                         0) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
-            return 1;
-        grid[dev] = per_cu * cus;
-    }
-    int G = grid[dev];
+    static std::atomic<int> grid[kMaxDevices];
+    int G = cached_per_device(grid, [](int dev) { return resident_grid(reinterpret_cast<const void*>(gemm_dma_sk_kernel<C, false>), C::THREADS, dev); });
+    if (G <= 0) return 1;
     if (ntiles * (C::BM == 128 ? 2 : 4) > G) return 1;
     // 16-bit 128x128 tiles above a quarter of the resident workgroups split only into segments of
     // at least 32 k-tiles, or when the tile grid is one row or one column (each tile then streams
@@ -1224,6 +1216,7 @@ static int run_dma_sk(const GemmDesc& d, hipStream_t stream, int group_m, int ti
     sk.dp_tiles = 0; // every tile is split here (at most a quarter as many tiles as workgroups)
     sk.wgs = G;
     const int rc = gemm_sk_workspace(stream, (size_t)ntiles, (size_t)2 * G * sk_slot_bytes<C>(), &sk.cnt, &sk.slots);
+    if (rc == TV_E_NOMEM) return 1; // no room for the slots: one workgroup per tile serves the call
     if (rc) return rc;
     hipLaunchKernelGGL((gemm_dma_sk_kernel<C, FUSED>), dim3((unsigned)G), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n, group_m,
                        c_vec, sk);
@@ -1292,14 +1285,12 @@ static int run_smallk_cfg(const GemmDesc& d, hipStream_t stream) {
 
 // Compute units of the current device (cached per device; 256 if the runtime cannot tell).
 static int device_cus() {
-    static int cached[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] <= 0) {
+    static std::atomic<int> cached[kMaxDevices];
+    const int v = cached_per_device(cached, [](int dev) {
         int cus = 0;
-        cached[dev] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0 ? cus : 256;
-    }
-    return cached[dev];
+        return hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0 ? cus : 0;
+    });
+    return v > 0 ? v : 256;
 }
 
 // The 16-bit small-K path: 128x128 tiles, groups of ceil(tiles_n / 2) persistent workgroups (one

@@ -1,4 +1,5 @@
-// __bf16 instantiation of the MFMA GEMM kernels (gemm_mfma_impl.h).
+// __bf16 instantiation of the GEMM kernels: the direct-load kernels of gemm_dma_impl.h and, for the
+// operand layouts they do not take, the register-staged kernels of gemm_mfma_impl.h (which it includes).
 #include "gemm_dma_impl.h"
 
 namespace tvk {

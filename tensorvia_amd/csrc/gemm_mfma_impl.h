@@ -849,17 +849,15 @@ void gemm_mfma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int 
 // cached per device; 0 if the runtime cannot tell.
 template <class C>
 static int sk_grid() {
-    static int cached[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (cached[dev] > 0) return cached[dev];
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(gemm_mfma_sk_kernel<C, false>), C::THREADS, 0) !=
-            hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
-        return 0;
-    cached[dev] = per_cu * cus;
-    return cached[dev];
+    static std::atomic<int> cached[kMaxDevices];
+    return cached_per_device(cached, [](int dev) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(gemm_mfma_sk_kernel<C, false>),
+                                                         C::THREADS, 0) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
+            return 0;
+        return per_cu * cus;
+    });
 }
 
 // The stream-K launch: K of at least 32 k-tiles (8 when the tiles do not fill the CUs), at least 8
@@ -889,6 +887,7 @@ static int run_cfg_sk(const GemmDesc& d, hipStream_t stream, int group_m, int ti
     sk.dp_tiles = (int)dp;
     sk.wgs = wgs;
     const int rc = gemm_sk_workspace(stream, (size_t)ntiles, (size_t)2 * G * sk_slot_bytes<C>(), &sk.cnt, &sk.slots);
+    if (rc == TV_E_NOMEM) return 1; // no room for the slots: one workgroup per tile serves the call
     if (rc) return rc;
     hipLaunchKernelGGL((gemm_mfma_sk_kernel<C, FUSED>), dim3((unsigned)G), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n,
                        group_m, c_vec, sk);

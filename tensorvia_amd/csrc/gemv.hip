@@ -699,6 +699,19 @@ struct GemvWorkspace {
 static std::mutex g_ws_mu;
 static std::map<std::tuple<int, hipStream_t, int>, GemvWorkspace> g_ws;
 
+// Test hook (tv_hip_inject_alloc_failure): while armed, each workspace request allocates, asking the
+// runtime for more memory than any device has, so it fails as it would under memory pressure (a
+// buffer the stream already holds is kept for later requests).
+static std::atomic<int> g_alloc_fail{0};
+constexpr size_t kImpossibleBytes = (size_t)1 << 60;
+static bool alloc_failure_armed() {
+    int n = g_alloc_fail.load();
+    while (n > 0)
+        if (g_alloc_fail.compare_exchange_weak(n, n - 1)) return true;
+    return false;
+}
+void inject_alloc_failure(int count) { g_alloc_fail.store(count < 0 ? 0 : count); }
+
 // kind 1: the GEMV's split-K arrival counters (every launch leaves them at zero); kind 2: its strip
 // partial slots; kinds 3 and 4: the same for the stream-K GEMM schedule (gemm_sk_workspace); kinds
 // 5 and 6: the zero-padded copies of GEMM operands A and B (gemm_pad_workspace).
@@ -708,8 +721,9 @@ static int get_workspace(hipStream_t stream, size_t need, void** out, int kind) 
     if (e != hipSuccess) return e;
     std::lock_guard<std::mutex> lk(g_ws_mu);
     GemvWorkspace& w = g_ws[{dev, stream, kind}];
-    if (w.bytes < need) {
-        if (w.base) {
+    const bool fail = alloc_failure_armed(); // test hook: this request fails as an allocation would
+    if (w.bytes < need || fail) {
+        if (w.base && !fail) {
             // The old buffer may still be in use by queued work of this stream.
             e = hipStreamSynchronize(stream);
             if (e != hipSuccess) return e;
@@ -718,8 +732,16 @@ static int get_workspace(hipStream_t stream, size_t need, void** out, int kind) 
             w.bytes = 0;
         }
         const size_t sz = need < ((size_t)1 << 20) ? ((size_t)1 << 20) : need;
-        e = hipMalloc(&w.base, sz);
-        if (e != hipSuccess) return TV_E_NOMEM;
+        void* p = nullptr;
+        e = hipMalloc(&p, fail ? kImpossibleBytes : sz);
+        if (e != hipSuccess) {
+            // The caller may carry on without the buffer (another kernel, the gather loader): the
+            // failed allocation must not stay behind as the runtime's last error, which the
+            // launchers report after their launch.
+            (void)hipGetLastError();
+            return TV_E_NOMEM;
+        }
+        w.base = p;
         w.bytes = sz;
         // The arrival counters must start at zero (each launch leaves them at zero again).  This
         // workspace is not meant for stream capture: growing it synchronises the stream.
@@ -982,12 +1004,6 @@ static int launch_gemv_plan_with(const GemmDesc& d, hipStream_t stream, const Ge
         case TV_INT8: return gemv_dispatch_mr<int8_t>(d, stream, p, fixed);
         default: return TV_E_UNSUPPORTED;
     }
-}
-
-int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices) {
-    if (!gemv_layout_ok(d) || d.M > 8) return TV_E_UNSUPPORTED; // the dot-product kernel: M <= 8
-    if (d.N == 0 || d.batch == 0) return 0;
-    return launch_gemv_plan_with(d, stream, GemvPlan{nl, threads, nslices}, nullptr);
 }
 
 // The matrix-core kernel serves 16-bit W at every M and int8 W at M >= 3, with whole 128-byte

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "tensorvia_hip.h"
 
 namespace tvk {
@@ -81,7 +83,10 @@ __host__ __device__ inline ActCoef act_coef(int act) {
 __device__ inline float act_logistic(float x, const ActCoef& k) {
     // 2^(l*x) overflows to +inf for large -x: s = rcp(inf) = 0, the limit.
     const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(k.l * x));
-    return (k.a * x + k.c) * s + k.e;
+    // sigmoid and tanh have a = 0: the a*x term is left out rather than multiplied, since 0 * inf
+    // would turn their limits at x = +-inf (1 and 0, +-1) into NaN.
+    const float ax = k.a != 0.0f ? k.a * x : 0.0f;
+    return (ax + k.c) * s + k.e;
 }
 __device__ inline float act_simple(float x, int act) { return act == TV_ACT_RELU ? (x > 0.0f ? x : 0.0f) : x; }
 __device__ inline float act_apply(float x, int act) {
@@ -167,6 +172,8 @@ int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream, bool may_alloc = tru
 // zero-padded rows in the per-stream workspace (calls of at least 2^20 multiply-adds or K >= 256) and points d
 // at the copies (pad_a / pad_b).  0 with d unchanged when nothing needs or gets a copy.
 int pad_gemm_operands(GemmDesc& d, hipStream_t stream);
+// The next `count` workspace allocations fail (tv_hip_inject_alloc_failure).
+void inject_alloc_failure(int count);
 // Per-(device, stream) buffers of the stream-K GEMM schedule: `cnt_ints` arrival counters (zero
 // between launches) and `slot_bytes` of partial-accumulator slots.
 int gemm_sk_workspace(hipStream_t stream, size_t cnt_ints, size_t slot_bytes, int** cnt, char** slots);
@@ -191,8 +198,6 @@ int launch_gemv(const GemmDesc& d, hipStream_t stream, const GemvScratch* fixed 
 // The static split-K scratch of the current device (set up on its first use: its address is looked
 // up and its counters cleared on `stream`).
 int gemv_static_scratch(hipStream_t stream, GemvScratch* out);
-// GEMV with an explicit strip width (nl lanes), workgroup size and K split (tuning sweeps).
-int launch_gemv_plan(const GemmDesc& d, hipStream_t stream, int nl, int threads, int nslices);
 // Zero-padded row copy of a GEMM operand: nb batches (source stride s_batch) of `rows` rows (source
 // stride s_row) of L contiguous elements of `es` bytes, written densely as rows of P elements (P a
 // multiple of 16 bytes), zero in [L, P).
@@ -200,6 +205,22 @@ int launch_pad_rows(const void* src, void* dst, int es, int64_t nb, int64_t rows
                     int64_t L, int64_t P, hipStream_t stream);
 // Per-(device, stream) buffer for the padded copy of operand A (operand 0) or B (operand 1).
 int gemm_pad_workspace(hipStream_t stream, size_t bytes, int operand, void** out);
+
+// A value computed once per device by host code (a resident-workgroup grid, a CU count), 0 while it
+// is not known.  Relaxed atomic loads and stores: host threads making their first calls at the same
+// time may each compute it, and each stores the same value.  Returns 0 if the device cannot be
+// named or compute() fails (returns 0 or less).
+constexpr int kMaxDevices = 64;
+template <class F> inline int cached_per_device(std::atomic<int> (&slot)[kMaxDevices], F&& compute) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+    int v = slot[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    v = compute(dev);
+    if (v <= 0) return 0;
+    slot[dev].store(v, std::memory_order_relaxed);
+    return v;
+}
 
 // Buffer loads: a lane offset at or above 2^31 is outside every buffer resource built by make_rsrc
 // (num_records <= 2^30), also after a stride multiple below 2^30 is added to it, and such a load

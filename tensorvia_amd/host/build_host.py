@@ -35,4 +35,21 @@ def build(verbose: bool = False) -> Path:
              f"-L{be.PKG}", "-ltv_hip", f"-L{ROCM}/lib", "-lamdhip64", "-pthread",
              "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM}/lib"], verbose)
     os.replace(tmp, be.HOST_LIB)
+    build_tools(verbose)
     return be.HOST_LIB
+
+
+# Programs built on libtensorvia.so: ops_mul_time times ops::Mul end to end as the reference's
+# tests/mul.cpp does (bench.py runs it).
+TOOLS = ["ops_mul_time"]
+BIN = be.PKG / "bin"
+
+
+def build_tools(verbose: bool = False) -> None:
+    BIN.mkdir(exist_ok=True)
+    for prog in TOOLS:
+        out = BIN / prog
+        tmp = out.with_suffix(".tmp")
+        be._run([CXX, *CXXFLAGS, str(HOST / (prog + ".cpp")), "-o", str(tmp), f"-L{be.PKG}", "-ltensorvia", "-ltv_hip",
+                 f"-L{ROCM}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN/..", f"-Wl,-rpath,{ROCM}/lib"], verbose)
+        os.replace(tmp, out)

@@ -4,6 +4,7 @@
 // on the C-ABI of include/tensorvia_hip.h.
 #include <algorithm>
 #include <condition_variable>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -49,6 +50,81 @@ HIPContext::HIPContext() {
     }
     hip_check(hipSetDevice(m_device_id), "hipSetDevice");
     hip_check(hipStreamCreate(&m_stream), "hipStreamCreate");
+    size_t free_b = 0, total_b = 0;
+    m_cache_limit = hipMemGetInfo(&free_b, &total_b) == hipSuccess ? total_b / 4 : (size_t(1) << 30);
+    if (const char* env = std::getenv("TV_HIP_CACHE_LIMIT_MB")) {
+        char* end = nullptr;
+        const unsigned long long mb = std::strtoull(env, &end, 10);
+        if (end != env) m_cache_limit = static_cast<size_t>(mb) << 20;
+    }
+}
+
+// ---- device block cache ----------------------------------------------------------------------------
+
+namespace {
+size_t round_block(size_t bytes) {
+    const size_t g = bytes < (size_t(1) << 20) ? 512 : (size_t(2) << 20);
+    return (bytes + g - 1) / g * g;
+}
+} // namespace
+
+void* HIPContext::alloc(size_t bytes, size_t* capacity) {
+    *capacity = 0;
+    if (bytes == 0) return nullptr;
+    const size_t want = round_block(bytes);
+    {
+        std::lock_guard<std::mutex> lk(m_cache_mu);
+        auto it = m_free.lower_bound(want);
+        if (it != m_free.end() && it->first <= want + want / 4) {
+            void* p = it->second;
+            *capacity = it->first;
+            m_cached -= it->first;
+            m_free.erase(it);
+            return p;
+        }
+    }
+    hip_check(hipSetDevice(m_device_id), "hipSetDevice");
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        empty_cache();
+        e = hipMalloc(&p, want);
+    }
+    hip_check(e, "hipMalloc");
+    *capacity = want;
+    return p;
+}
+
+void HIPContext::release(void* p, size_t capacity) {
+    if (!p) return;
+    {
+        std::lock_guard<std::mutex> lk(m_cache_mu);
+        if (m_cached + capacity <= m_cache_limit) {
+            m_free.emplace(capacity, p);
+            m_cached += capacity;
+            return;
+        }
+    }
+    (void)hipStreamSynchronize(m_stream); // work queued on the block finishes before it is freed
+    (void)hipFree(p);
+}
+
+void HIPContext::empty_cache() {
+    std::multimap<size_t, void*> blocks;
+    {
+        std::lock_guard<std::mutex> lk(m_cache_mu);
+        blocks.swap(m_free);
+        m_cached = 0;
+    }
+    if (blocks.empty()) return;
+    (void)hipStreamSynchronize(m_stream);
+    for (auto& b : blocks) (void)hipFree(b.second);
+}
+
+size_t HIPContext::cached_bytes() const {
+    std::lock_guard<std::mutex> lk(m_cache_mu);
+    return m_cached;
 }
 
 // ---- ParallelMemcpy ------------------------------------------------------------------------------
@@ -134,6 +210,8 @@ static constexpr size_t kStagingMin = size_t(4) << 20;
 
 HIPContext::~HIPContext() {
     if (m_stream) (void)hipStreamSynchronize(m_stream);
+    for (auto& b : m_free) (void)hipFree(b.second);
+    m_free.clear();
     m_staging.reset();
     if (m_stream) (void)hipStreamDestroy(m_stream);
 }
@@ -218,17 +296,11 @@ std::shared_ptr<HIPContext> HIPContext::get() {
 HIPTensor::HIPTensor(void* host_ptr, size_t numel, DataType dtype, std::shared_ptr<HIPContext> ctx)
     : m_numel(numel), m_dtype(dtype), m_context(std::move(ctx)) {
     const size_t bytes = numel * calc_dtype_size(dtype);
-    hip_check(hipSetDevice(m_context->device_id()), "hipSetDevice");
-    hip_check(hipMalloc(&m_data, bytes), "hipMalloc");
-    if (host_ptr) m_context->copy_h2d(m_data, host_ptr, bytes);
+    m_data = m_context->alloc(bytes, &m_capacity);
+    if (host_ptr && bytes) m_context->copy_h2d(m_data, host_ptr, bytes);
 }
 
-HIPTensor::~HIPTensor() {
-    if (m_data) {
-        (void)hipStreamSynchronize(m_context->stream());
-        (void)hipFree(m_data);
-    }
-}
+HIPTensor::~HIPTensor() { m_context->release(m_data, m_capacity); }
 
 void HIPTensor::copy_to(std::shared_ptr<TensorImpl> dst) const {
     const size_t bytes = m_numel * calc_dtype_size(m_dtype);
@@ -434,11 +506,12 @@ void TransposeImpl<Device::HIP>::execute(const Tensor& a, Tensor& dst, std::init
         throw std::runtime_error("Transpose: dst dtype " + std::string(dtype_to_string(dst.dtype())) +
                                  " differs from the input's " + std::string(dtype_to_string(a.dtype())));
     const Tensor view = a.permute(std::vector<int64_t>(axes));
-    std::vector<int64_t> shape = view.shape();
-    dst.reshape(shape); // as the reference (src/backend/cuda/transpose.cu:129-134); dst is dense after it
+    // Both checks come before dst is touched: a caller that catches the error keeps dst as it was.
     if (view.dims() > TV_MAX_DIMS) throw std::runtime_error("Transpose: too many dimensions");
     // A permutation written over its own source would read elements it has already overwritten.
     if (dst.get_impl() == a.get_impl()) throw std::runtime_error("Transpose: dst shares storage with a");
+    std::vector<int64_t> shape = view.shape();
+    dst.reshape(shape); // as the reference (src/backend/cuda/transpose.cu:129-134); dst is dense after it
     const size_t es = calc_dtype_size(a.dtype());
     tv_repack_args r{};
     r.ndim = static_cast<int32_t>(view.dims());

@@ -224,3 +224,36 @@ def test_no_epilogue_equals_plain_gemm():
     tv.check(tv.lib().tv_hip_gemm_ex(ctypes.byref(args), ctypes.byref(ep), s))
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("act", [tv.ACT_RELU, tv.ACT_SILU, tv.ACT_SIGMOID, tv.ACT_TANH], ids=lambda a: ACT_NAMES[a])
+@pytest.mark.parametrize("dt,M,K,N", [(tv.FLOAT32, 64, 96, 80), (tv.BFLOAT16, 300, 256, 272), (tv.BFLOAT16, 1, 512, 128),
+                                      (tv.FLOAT32, 3, 512, 96)], ids=["f32_gemm", "bf16_gemm", "bf16_gemv", "f32_gemv"])
+def test_infinite_bias_gives_the_activation_limits(act, dt, M, K, N):
+    """A per-column bias of +inf / -inf in some columns: the activation's limits, as the reference's
+    composition gives them (sigmoid 1 / 0, tanh +1 / -1, relu inf / 0, silu inf / NaN)."""
+    import torch
+    a = rng.make("uniform", (M, K), 41, NAME[dt], -1, 1)
+    b = rng.make("uniform", (K, N), 42, NAME[dt], -1, 1)
+    bias = np.zeros(N, dtype=np.float32)
+    bias[0::4] = np.inf
+    bias[1::4] = -np.inf
+    bias_st = rng.f32_to_bf16_bits(bias) if dt == tv.BFLOAT16 else bias
+    ta, tb = storage_to_torch(a, dt), storage_to_torch(b, dt)
+    tbias = storage_to_torch(bias_st, dt)
+    tc = torch.zeros((M, N), dtype=ta.dtype, device="cuda")
+    args = tv.make_args(ta, tb, tc)
+    ep = tv.TvEpilogue()
+    ep.act = act
+    ep.bias = tbias.data_ptr()
+    ep.sbias_b, ep.sbias_m, ep.sbias_n = 0, 0, 1
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    tv.check(tv.lib().tv_hip_gemm_ex(ctypes.byref(args), ctypes.byref(ep), s))
+    torch.cuda.synchronize()
+    c = to_f64(torch_to_storage(tc), dt)
+    with np.errstate(all="ignore"):
+        pre = np.matmul(to_f64(a, dt), to_f64(b, dt)) + bias.astype(np.float64)
+        ref = ACTS[act](pre)
+    inf_cols = np.isinf(bias)
+    np.testing.assert_array_equal(c[:, inf_cols], ref[:, inf_cols])  # NaN == NaN here
+    assert np.isfinite(c[:, ~inf_cols]).all()
