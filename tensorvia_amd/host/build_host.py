@@ -50,6 +50,6 @@ def build_tools(verbose: bool = False) -> None:
     for prog in TOOLS:
         out = BIN / prog
         tmp = out.with_suffix(".tmp")
-        be._run([CXX, *CXXFLAGS, str(HOST / (prog + ".cpp")), "-o", str(tmp), f"-L{be.PKG}", "-ltensorvia", "-ltv_hip",
+        be._run([CXX, *CXXFLAGS, "-Werror=format", str(HOST / (prog + ".cpp")), "-o", str(tmp), f"-L{be.PKG}", "-ltensorvia", "-ltv_hip",
                  f"-L{ROCM}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN/..", f"-Wl,-rpath,{ROCM}/lib"], verbose)
         os.replace(tmp, out)

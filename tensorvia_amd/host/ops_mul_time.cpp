@@ -95,7 +95,7 @@ int main(int argc, char** argv) {
         std::printf("{\"shape\": [%lld, %lld, %lld], \"dtype\": \"%s\", \"iters\": %d, \"cache_limit_mb\": %zu, "
                     "\"ops_mul_ms\": %.4f, \"alloc_free_ms\": %.4f, \"kernel_ms\": %.4f, \"launch_sync_ms\": %.4f}\n",
                     static_cast<long long>(M), static_cast<long long>(K), static_cast<long long>(N),
-                    via::dtype_to_string(dt), iters, ctx->cache_limit() >> 20, mul_ms, alloc_ms, kernel_ms,
+                    std::string(via::dtype_to_string(dt)).c_str(), iters, ctx->cache_limit() >> 20, mul_ms, alloc_ms, kernel_ms,
                     mul_ms - alloc_ms - kernel_ms);
     } catch (const std::exception& e) {
         std::fprintf(stderr, "ops_mul_time: %s\n", e.what());
