@@ -158,6 +158,16 @@ def test_direct_load_256_tiles_fused(act, N, bt):
     run_case(tv.BFLOAT16, tv.BFLOAT16, 0, 2100, 256, N, "col", act, bt=bt, seed=41)
 
 
+@pytest.mark.parametrize("act", [tv.ACT_NONE, tv.ACT_RELU, tv.ACT_SILU, tv.ACT_TANH])
+@pytest.mark.parametrize("bias_kind,dt", [("col", tv.BFLOAT16), ("colb", tv.BFLOAT16), ("none", tv.FLOAT16)])
+def test_two_tiles_per_cu_fused(act, bias_kind, dt):
+    """Two or more 256x256 tiles per CU (8 x 8 x 8 = 512 here, the c3 layout at K = 256), where the
+    plain GEMM chains tiles: the fused call runs one workgroup per tile, with the per-column (per
+    batch) or no bias and the activation applied as the 16-bit output is staged.  Batches 0 and 7
+    are checked against the fp64 composition."""
+    run_case(dt, dt, 8, 2048, 256, 2048, bias_kind, act, seed=43, check=[0, 7])
+
+
 @pytest.mark.parametrize("act", [tv.ACT_RELU, tv.ACT_SILU])
 def test_bf16_in_fp32_out(act):
     run_case(tv.BFLOAT16, tv.FLOAT32, 0, 260, 320, 300, "col", act, seed=2)
