@@ -72,8 +72,25 @@ def build_kernels(verbose: bool = False, force: bool = True) -> Path:
     return KERNEL_LIB
 
 
+# Measurement programs (tensorvia_amd/bin/): lds_bank_probe issues one LDS access pattern of the
+# GEMM kernels per launch, for rocprofv3's LDS bank-conflict counter.
+PROBES = ["lds_bank_probe"]
+
+
+def build_probes(verbose: bool = False) -> None:
+    out_dir = PKG / "bin"
+    out_dir.mkdir(exist_ok=True)
+    for prog in PROBES:
+        out = out_dir / prog
+        tmp = out.with_suffix(".tmp")
+        _run([HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-Wall", *DEVICE_FLAGS,
+              str(CSRC / (prog + ".hip")), "-o", str(tmp)], verbose)
+        os.replace(tmp, out)
+
+
 def build(verbose: bool = False) -> None:
     build_kernels(verbose=verbose)
+    build_probes(verbose=verbose)
     host = PKG / "host"
     if (host / "build_host.py").exists():
         from .host import build_host  # noqa: WPS433
