@@ -63,6 +63,9 @@ def make_inputs(name: str):
     if name == "c3":
         return dict(a=rng.make("uniform", (16, 2048, 4096), 5, "bfloat16"),
                     b=rng.make("uniform", (4096, 4096), 6, "bfloat16"), dt=4)
+    if name == "bf16_4096":
+        return dict(a=rng.make("uniform", (4096, 4096), 13, "bfloat16"),
+                    b=rng.make("uniform", (4096, 4096), 14, "bfloat16"), dt=4)
     if name == "c4":
         q = rng.normal_f32(7, 32 * 2048 * 128) / np.float32(np.sqrt(128.0))
         k = rng.normal_f32(8, 32 * 2048 * 128) / np.float32(np.sqrt(128.0))
@@ -83,17 +86,20 @@ DESC = {
     "c2": "int8 A[4096,4096] @ B[4096,4096] -> int8 (low byte of the int32 sum)",
     "c3": "bf16 A[16,2048,4096] @ B[4096,4096] (B broadcast over batch) -> bf16, fp32 accumulate",
     "c3_fused": "c3 with the fused epilogue: silu(A @ B + bias[4096]) -> bf16 (tv_hip_gemm_ex)",
+    "bf16_4096": "bf16 A[4096,4096] @ B[4096,4096] -> bf16, fp32 accumulate (the bf16 4096^3 shape of the targets)",
     "c4": "fp16 Q[32,2048,128] @ K.permute(0,2,1) (strided view, no repack) -> fp16 [32,2048,2048]",
     "c5m1": "bf16 GEMV x[1,4096] @ W[4096,11008] -> bf16, fp32 accumulate (6 W replicas rotated)",
     "c5m8": "bf16 GEMV x[8,4096] @ W[4096,11008] -> bf16, fp32 accumulate (6 W replicas rotated)",
 }
-DTYPE = {"c1": "fp32", "c2": "int8", "c3": "bf16", "c3_fused": "bf16", "c4": "fp16", "c5m1": "bf16", "c5m8": "bf16"}
+DTYPE = {"c1": "fp32", "c2": "int8", "c3": "bf16", "c3_fused": "bf16", "bf16_4096": "bf16", "c4": "fp16", "c5m1": "bf16",
+         "c5m8": "bf16"}
 # The kernel each configuration's launch runs.
 KERNEL = {
     "c1": "gemm_mfma_sk_kernel<GemmCfg<float, 128, 128, 2, 2, 0, 1>, false> (stream-K schedule)",
     "c2": "gemm_dma_kernel<GemmCfg<signed char, 256, 256, 2, 4, 0, 1>, false>",
     "c3": "gemm_dma_chain_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>> (chained tiles)",
     "c3_fused": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, true>",
+    "bf16_4096": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, false>",
     "c4": "gemm_smallk_pipe_kernel<GemmCfg<_Float16, 128, 128, 2, 4, 0, 0>, _Float16> (row-synchronous groups)",
     "c5m1": "gemv_mfma_kernel<__bf16, 4, 2, 8>",
     "c5m8": "gemv_mfma_kernel<__bf16, 4, 2, 8>",
@@ -105,6 +111,7 @@ TRACE_KERNEL = {
     "c2": r"gemm_dma_kernel.*(GemmCfg<signed char, 256, 256|GemmCfgIaLi256ELi256E)",
     "c3": r"gemm_dma_chain_kernel.*(GemmCfg<__bf16|GemmCfgIDF16b)",
     "c3_fused": r"gemm_dma_kernel.*(GemmCfg<__bf16|GemmCfgIDF16b).*(true|Lb1E)",
+    "bf16_4096": r"gemm_dma_kernel.*(GemmCfg<__bf16|GemmCfgIDF16b).*(false|Lb0E)",
     "c4": r"gemm_smallk_pipe_kernel.*(GemmCfg<_Float16|GemmCfgIDF16_)",
     "c5m1": r"gemv_mfma_kernel.*(__bf16|DF16b)",
     "c5m8": r"gemv_mfma_kernel.*(__bf16|DF16b)",
@@ -113,7 +120,8 @@ TRACE_KERNEL = {
 }
 # Bound each configuration is judged against (c4's arithmetic intensity, 113.8 FLOP/B, is below
 # the fp16 ridge of about 315: HBM-bound).
-BOUND = {"c1": "mfma", "c2": "mfma", "c3": "mfma", "c3_fused": "mfma", "c4": "hbm", "c5m1": "hbm", "c5m8": "hbm"}
+BOUND = {"c1": "mfma", "c2": "mfma", "c3": "mfma", "c3_fused": "mfma", "bf16_4096": "mfma", "c4": "hbm", "c5m1": "hbm",
+         "c5m8": "hbm"}
 
 
 def work(name: str, inp) -> tuple[float, float]:
@@ -353,7 +361,8 @@ def run_copy(steps: int, warmup: int) -> dict:
 # once, as the equivalent flattened 2-d call [32768,4096] @ [4096,4096] (the reference rejects the
 # broadcast form, src/ops.cpp:544-550; about 17 s on 16 threads); c4 multiplies by a
 # pre-materialised K^T (the CPU kernel ignores strides), whose transpose is timed apart.
-CPU_PLAN = {"c1": (3, None), "c2": (3, None), "c3": (1, None), "c4": (3, None), "c5m1": (10, None), "c5m8": (10, None)}
+CPU_PLAN = {"c1": (3, None), "c2": (3, None), "c3": (1, None), "bf16_4096": (3, None), "c4": (3, None), "c5m1": (10, None),
+            "c5m8": (10, None)}
 
 
 def cpu_effective_threads(threads: int, batch: int, M: int, N: int) -> int:
@@ -488,7 +497,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="c1,c2,c3,c3_fused,c4,c5m1,c5m8,cast_c3a,random_c3a,fill_c3a,transpose_c4k")
+    ap.add_argument("--configs", default="c1,c2,c3,c3_fused,bf16_4096,c4,c5m1,c5m8,cast_c3a,random_c3a,fill_c3a,transpose_c4k")
     ap.add_argument("--only", default=None,
                     help="run only this config's GPU kernel (for profilers); 'copy' runs the traffic calibration copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
