@@ -19,8 +19,14 @@ using namespace via;
 
 namespace {
 
+// Throws on a failed HIP call.  The runtime also keeps the failure as its last error, which the
+// kernel library's launchers read after each launch: it is cleared here so that a caught exception
+// (an allocation that did not fit, say) is not reported again by the next, successful call.
 void hip_check(hipError_t e, const char* what) {
-    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+    }
 }
 
 void tv_check(int rc, const char* what) {

@@ -20,7 +20,9 @@
 //                    materialised K^T); i = 4 permutes the slice [1:3, 2:6, :] of the int32 source by
 //                    {2,1,0} (a view with an offset)
 //   "threw <name>" lines: calls that must throw (bias of the wrong dtype or shape; Transpose into a
-//   dst of another dtype or into a's own storage).
+//   dst of another dtype or into a's own storage; a 2^60-byte device tensor).
+//   mul_after_oom    ops::Mul(Random({64,96}, int8, -3, 3, 5), Random({96,80}, int8, -3, 3, 6)) right
+//                    after the failed allocation
 #include <cstdio>
 #include <fstream>
 #include <string>
@@ -138,6 +140,10 @@ int main(int argc, char** argv) {
     must_throw("transpose_dst_dtype", [&] { ops::Transpose(a, tdst_f32, {1, 0}); });
     Tensor self = ops::Random({8, 8}, DataType::FLOAT32, -1.0f, 1.0f, 7);
     must_throw("transpose_dst_self", [&] { ops::Transpose(self, self, {1, 0}); });
+    // A device allocation that cannot fit throws, and leaves nothing behind that the next op would
+    // report: ops::Mul right after it must succeed.
+    must_throw("alloc_too_large", [&] { Tensor huge({int64_t(1) << 58}, DataType::FLOAT32, via::Device::HIP); });
+    run("mul_after_oom", [&] { return ops::Mul(ai, bi); });
     std::printf("failures %d\n", failures);
     return failures ? 1 : 0;
 }

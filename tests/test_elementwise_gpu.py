@@ -163,6 +163,19 @@ def test_cpp_transpose_into_dst_errors(init_run):
         assert re.search(rf"^threw {name}: ", r.stdout, re.M), r.stdout[-2000:]
 
 
+def test_cpp_failed_allocation_leaves_no_error_behind(init_run):
+    """A device tensor too large for the device throws (the reference's CUDA backend throws the
+    driver's message, include/backend/cuda/cuda_tensor.cpp:20-23), and the int8 ops::Mul that
+    follows succeeds with the exact low-byte result: the failure is not reported again."""
+    r, out, done = init_run
+    assert re.search(r"^threw alloc_too_large: .*hipMalloc", r.stdout, re.M), r.stdout[-2000:]
+    assert "mul_after_oom" in done, r.stdout[-2000:]
+    a = rng.make("uniform", (64, 96), 5, "int8", -3, 3)
+    b = rng.make("uniform", (96, 80), 6, "int8", -3, 3)
+    want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.int8)
+    np.testing.assert_array_equal(_read(out, "mul_after_oom", INT8, (64, 80)), want)
+
+
 def test_cpp_init_driver_exit_status(init_run):
     r, _, _ = init_run
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]

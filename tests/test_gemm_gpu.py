@@ -246,6 +246,23 @@ def test_bf16_config3_full_size_broadcast_equals_flattened(hip):
     assert_half_close(c, ref, orc.abs_bound(to_f32(xa, BFLOAT16), to_f32(b, BFLOAT16)), K)
 
 
+def test_bf16_4096_full_size_sampled(hip):
+    """bf16 [4096,4096] @ [4096,4096] (the bf16 4096^3 throughput shape, bench.py's inputs: seeds 13
+    and 14, U[-1,1]; 256 output tiles, one per CU): 48 sampled rows and 48 sampled columns against
+    the oracle under the bf16 bar."""
+    n = 4096
+    a = rng.make("uniform", (n, n), 13, "bfloat16")
+    b = rng.make("uniform", (n, n), 14, "bfloat16")
+    c = to_f32(to_storage(hip.gemm(to_torch(a, BFLOAT16), to_torch(b, BFLOAT16))), BFLOAT16)
+    r = np.random.default_rng(3)
+    rows = r.choice(n, 48, replace=False)
+    cols = r.choice(n, 48, replace=False)
+    fa, fb = to_f32(a, BFLOAT16), to_f32(b, BFLOAT16)
+    assert_half_close(c[rows], orc.mul(a[rows], BFLOAT16, b, BFLOAT16), orc.abs_bound(fa[rows], fb), n)
+    bc = np.ascontiguousarray(b[:, cols])
+    assert_half_close(c[:, cols], orc.mul(a, BFLOAT16, bc, BFLOAT16), orc.abs_bound(fa, fb[:, cols]), n)
+
+
 def test_fp16_config4_transposed_view(hip):
     """c4 at full size: Q[32,2048,128] @ K.permute(0,2,1) consumed through strides (the persistent
     small-K path), against the oracle on the materialised transpose (ops::Transpose(K,{0,2,1}) on
