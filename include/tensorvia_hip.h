@@ -5,6 +5,9 @@
  * It carries plain pointers, sizes and element strides only: no C++ types, no exceptions,
  * no tensor allocation.  Every entry point returns 0 on success, a positive hipError_t value
  * when the HIP runtime failed, or a negative TV_E_* code when the arguments were rejected.
+ * Launch errors are read from the HIP runtime's last error of the calling thread, which each call
+ * that launches work clears on entry: an error that earlier, unrelated HIP calls left there is
+ * discarded, not reported as this call's.
  *
  * Reference interfaces replaced (paths into Aimol-l/Tensorvia):
  *   tv_hip_gemm   <- template<> struct MulImpl<Device::CUDA> { static Tensor execute(a, b); }

@@ -10,7 +10,13 @@ namespace {
 std::atomic<int> g_fault_code{0};
 std::atomic<int> g_fault_count{0};
 
-bool take_fault(int* code) {
+// Entry of every C-ABI call that launches work.  A launch's error is read back from the HIP
+// runtime's last error after the launch, so a failure that earlier, unrelated HIP calls of this
+// thread left there (and nobody read) is cleared first: the call's return code then reports its
+// own launches only.  Then the test hook: *code is set and true returned while injected faults
+// remain.
+bool enter_call(int* code) {
+    (void)hipGetLastError();
     int n = g_fault_count.load();
     while (n > 0) {
         if (g_fault_count.compare_exchange_weak(n, n - 1)) {
@@ -122,7 +128,7 @@ void tv_hip_inject_alloc_failure(int count) { tvk::inject_alloc_failure(count); 
 
 int tv_hip_gemm(const tv_gemm_args* args, void* hip_stream) {
     int code;
-    if (take_fault(&code)) return code;
+    if (enter_call(&code)) return code;
     tvk::GemmDesc d;
     int rc = validate(args, &d);
     if (rc) return rc;
@@ -131,7 +137,7 @@ int tv_hip_gemm(const tv_gemm_args* args, void* hip_stream) {
 
 int tv_hip_gemm_noalloc(const tv_gemm_args* args, void* hip_stream) {
     int code;
-    if (take_fault(&code)) return code;
+    if (enter_call(&code)) return code;
     tvk::GemmDesc d;
     int rc = validate(args, &d);
     if (rc) return rc;
@@ -144,7 +150,7 @@ int tv_hip_gemm_noalloc(const tv_gemm_args* args, void* hip_stream) {
 
 int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_stream) {
     int code;
-    if (take_fault(&code)) return code;
+    if (enter_call(&code)) return code;
     tvk::GemmDesc d;
     int rc = validate(args, &d);
     if (rc) return rc;
@@ -173,7 +179,7 @@ int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_st
 
 int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream) {
     int code;
-    if (take_fault(&code)) return code;
+    if (enter_call(&code)) return code;
     tvk::GemmDesc d;
     int rc = validate(args, &d);
     if (rc) return rc;
@@ -186,7 +192,7 @@ int tv_hip_gemv(const tv_gemm_args* args, void* hip_stream) {
 
 int tv_hip_repack(const tv_repack_args* args, void* hip_stream) {
     int code;
-    if (take_fault(&code)) return code;
+    if (enter_call(&code)) return code;
     if (!args) return TV_E_NULL;
     if (args->ndim < 0 || args->ndim > TV_MAX_DIMS) return TV_E_SHAPE;
     if (args->elem_size != 1 && args->elem_size != 2 && args->elem_size != 4 && args->elem_size != 8) return TV_E_DTYPE;
@@ -202,7 +208,7 @@ int tv_hip_repack(const tv_repack_args* args, void* hip_stream) {
 
 int tv_hip_typecast(const void* src, int32_t src_dtype, void* dst, int32_t dst_dtype, int64_t n, void* hip_stream) {
     int code;
-    if (take_fault(&code)) return code;
+    if (enter_call(&code)) return code;
     if (src_dtype < TV_INT8 || src_dtype > TV_FLOAT64 || dst_dtype < TV_INT8 || dst_dtype > TV_FLOAT64) return TV_E_DTYPE;
     if (n < 0) return TV_E_SHAPE;
     if (n == 0) return TV_OK;
@@ -215,7 +221,7 @@ int tv_hip_typecast(const void* src, int32_t src_dtype, void* dst, int32_t dst_d
 
 int tv_hip_fill(void* dst, int32_t dtype, int64_t n, float value, void* hip_stream) {
     int code;
-    if (take_fault(&code)) return code;
+    if (enter_call(&code)) return code;
     if (dtype < TV_INT8 || dtype > TV_FLOAT64) return TV_E_DTYPE;
     if (n < 0) return TV_E_SHAPE;
     if (n == 0) return TV_OK;
@@ -225,7 +231,7 @@ int tv_hip_fill(void* dst, int32_t dtype, int64_t n, float value, void* hip_stre
 
 int tv_hip_random(void* dst, int32_t dtype, int64_t n, float min, float max, uint64_t seed, void* hip_stream) {
     int code;
-    if (take_fault(&code)) return code;
+    if (enter_call(&code)) return code;
     if (dtype < TV_INT8 || dtype > TV_FLOAT64) return TV_E_DTYPE;
     if (n < 0 || !(min <= max)) return TV_E_SHAPE;
     if (n == 0) return TV_OK;

@@ -79,6 +79,32 @@ def test_failed_workspace_allocation_falls_back(hip, case):
     np.testing.assert_array_equal(got, want, err_msg=f"{name}: workspace path")
 
 
+def test_earlier_hip_failure_is_not_reported_as_the_call_s(hip):
+    """An error that an unrelated HIP call left as the thread's last error (a hipMalloc too large for
+    any device, unchecked) is not returned by the next tv_hip_gemm, whose own launch succeeds, and
+    the result is exact."""
+    hiprt = ctypes.CDLL("libamdhip64.so.7")  # by soname: the runtime already loaded, not a second copy
+    hiprt.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hiprt.hipMalloc.restype = ctypes.c_int
+    hiprt.hipGetLastError.restype = ctypes.c_int
+    a, b = _int_operands(INT8, (64, 96), (96, 80), 950, -3, 3)
+    ta, tb = to_torch(a, INT8), to_torch(b, INT8)
+    tc = torch.zeros((64, 80), dtype=torch.int8, device="cuda")
+    args = tv.make_args(ta, tb, tc)
+    stream = torch.cuda.current_stream()
+    stream.synchronize()
+    # No torch call between the planted failure and the library's call: torch reads the last error
+    # after its own launches too.
+    p = ctypes.c_void_p()
+    assert hiprt.hipMalloc(ctypes.byref(p), 1 << 60) != 0  # fails, and stays as the last error
+    rc = tv.lib().tv_hip_gemm(ctypes.byref(args), ctypes.c_void_p(stream.cuda_stream))
+    last = hiprt.hipGetLastError()
+    assert rc == tv.TV_OK, tv.strerror(rc)
+    assert last == 0
+    stream.synchronize()
+    np.testing.assert_array_equal(to_storage(tc), _exact(INT8, a, b))
+
+
 def test_noalloc_on_padded_skinny_float_call(hip):
     """bf16 x[1,4096] @ W[4096,129], random values: the padded matrix-core GEMV (tv_hip_gemm) and
     the in-place GEMM (tv_hip_gemm_noalloc) sum K in different orders; both are within the bf16 bar
