@@ -95,7 +95,7 @@ DTYPE = {"c1": "fp32", "c2": "int8", "c3": "bf16", "c3_fused": "bf16", "bf16_409
          "c5m8": "bf16"}
 # The kernel each configuration's launch runs.
 KERNEL = {
-    "c1": "gemm_mfma_sk_kernel<GemmCfg<float, 128, 128, 2, 2, 0, 1>, false> (stream-K schedule)",
+    "c1": "gemm_mfma_sk_kernel<GemmCfg<float, 96, 128, 2, 2, 0, 1>, false> (stream-K schedule)",
     "c2": "gemm_dma_kernel<GemmCfg<signed char, 256, 256, 2, 4, 0, 1>, false>",
     "c3": "gemm_dma_chain_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>> (chained tiles)",
     "c3_fused": "gemm_dma_kernel<GemmCfg<__bf16, 256, 256, 2, 4, 0, 1>, true>",
@@ -107,7 +107,7 @@ KERNEL = {
 # The same kernels as they appear in a rocprofv3 kernel trace (demangled, or mangled where the
 # profiler's demangler gives up on __bf16 / _Float16 template arguments).
 TRACE_KERNEL = {
-    "c1": r"gemm_mfma_sk_kernel.*(GemmCfg<float, 128, 128|GemmCfgIfLi128ELi128E)",
+    "c1": r"gemm_mfma_sk_kernel.*(GemmCfg<float, 96, 128|GemmCfgIfLi96ELi128E)",
     "c2": r"gemm_dma_kernel.*(GemmCfg<signed char, 256, 256|GemmCfgIaLi256ELi256E)",
     "c3": r"gemm_dma_chain_kernel.*(GemmCfg<__bf16|GemmCfgIDF16b)",
     "c3_fused": r"gemm_dma_kernel.*(GemmCfg<__bf16|GemmCfgIDF16b).*(true|Lb1E)",

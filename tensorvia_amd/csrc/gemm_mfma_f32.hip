@@ -13,17 +13,29 @@ namespace tvk {
 // 16) timed on every tile, where the cheapest lands 0.8 % from the fastest on average.  E.g. A[3000, 4096] @
 // B[4096, 129]: 128x128 84.5 us, 128x64 60.6 us, 128x32 56.6 us; A[8192, 4096] @ B[4096, 32]:
 // 128x64 51.4 us, 128x32 34.8 us; A[300, 4096] @ B[4096, 4096]: 128x128 116.1 us, 64x128 99.7 us.
+// A sixth tile, 96x128 (rate 0.984), serves row counts that 96 divides better than 128: on
+// A[2592, 2048] @ B[2048, 4096] it computes 2,592 rows instead of 2,688 and ran 341.5-342.7 us
+// against 348.5-349.1 us for 128x128 (same box, same process).  Its loaders need A k-contiguous
+// (96 rows of an m-contiguous A do not split into whole 16-byte chunks per thread).
 namespace {
 struct F32Tile {
     int bm, bn;
     double rate;
 };
-constexpr F32Tile kF32Tiles[5] = {{128, 128, 1.0}, {64, 128, 0.96}, {128, 64, 0.94}, {32, 128, 0.83}, {128, 32, 0.77}};
+constexpr int kF32TileCount = 6;
+constexpr F32Tile kF32Tiles[kF32TileCount] = {{128, 128, 1.0}, {64, 128, 0.96}, {128, 64, 0.94},
+                                              {32, 128, 0.83}, {128, 32, 0.77}, {96, 128, 0.984}};
+
+int f32_a_mode_96(const GemmDesc& d) { return pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, 4, 96, d.pad_a); }
+int f32_b_mode(const GemmDesc& d) { return pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, 4, 128, d.pad_b); }
 
 int pick_f32_tile(const GemmDesc& d) {
+    const int bm = f32_b_mode(d);
+    const bool t96_ok = f32_a_mode_96(d) == LOAD_KCONTIG && (bm == LOAD_MNCONTIG || bm == LOAD_KCONTIG);
     int best = 0;
     double best_cost = 0;
-    for (int i = 0; i < 5; ++i) {
+    for (int i = 0; i < kF32TileCount; ++i) {
+        if (i == 5 && !t96_ok) continue;
         const F32Tile& t = kF32Tiles[i];
         const double tm = (double)((d.M + t.bm - 1) / t.bm), tn = (double)((d.N + t.bn - 1) / t.bn);
         const double tiles = (double)d.batch * tm * tn;
@@ -44,7 +56,11 @@ int launch_gemm_mfma_f32(const GemmDesc& d, hipStream_t stream, bool may_alloc) 
         case 1: return run_modes<float, 64, 128, 2, 2>(d, stream, 8, may_alloc);
         case 2: return run_modes<float, 128, 64, 2, 2>(d, stream, 8, may_alloc);
         case 3: return run_modes<float, 32, 128, 1, 4>(d, stream, 8, may_alloc);
-        default: return run_modes<float, 128, 32, 4, 1>(d, stream, 8, may_alloc);
+        case 4: return run_modes<float, 128, 32, 4, 1>(d, stream, 8, may_alloc);
+        default:
+            if (f32_b_mode(d) == LOAD_MNCONTIG)
+                return run_cfg<GemmCfg<float, 96, 128, 2, 2, LOAD_KCONTIG, LOAD_MNCONTIG>>(d, stream, 8, may_alloc);
+            return run_cfg<GemmCfg<float, 96, 128, 2, 2, LOAD_KCONTIG, LOAD_KCONTIG>>(d, stream, 8, may_alloc);
     }
 }
 } // namespace tvk

@@ -729,8 +729,8 @@ void gemm_mfma_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c_v
 
 // ---------------------------------------------------------------------------------------------
 // Stream-K schedule (fp32): G resident workgroups share the work instead of one workgroup per
-// tile.  Every CU then does the same work however the tiles divide over the CUs (c1: 672 tiles of
-// 128x128 on 256 CUs, 2.625 per CU, which the one-per-tile launch runs in the time of 3), and fewer
+// tile.  Every CU then does the same work however the tiles divide over the CUs (c1: 864 tiles of
+// 96x128 on 256 CUs, 3.375 per CU, which the one-per-tile launch runs in the time of 4), and fewer
 // tiles than CUs still use every CU.  Whole rounds of G tiles run whole (workgroup w takes tiles
 // w, w + G, ...), so the workgroups running side by side take neighbouring tiles at the same k and
 // share their operands in L2; the last, partial round is split: the first `wgs` workgroups take

@@ -114,6 +114,14 @@ def test_fp32_mfma_kernel(act, bias_kind):
     run_case(tv.FLOAT32, tv.FLOAT32, 0, 200, 96, 130, bias_kind, act)
 
 
+@pytest.mark.parametrize("act", [tv.ACT_RELU, tv.ACT_SILU, tv.ACT_SIGMOID])
+@pytest.mark.parametrize("bias_kind", ["col", "full", "none"])
+def test_fp32_96_row_tile(act, bias_kind):
+    """fp32 A[1340, 264] @ B[264, 2100]: the tile cost rule picks the 96x128 tile (238 tiles, the
+    last row of tiles 92 rows high); the fused epilogue on it."""
+    run_case(tv.FLOAT32, tv.FLOAT32, 0, 1340, 264, 2100, bias_kind, act, seed=41)
+
+
 @pytest.mark.parametrize("act", list(ACTS), ids=lambda a: ACT_NAMES[a])
 @pytest.mark.parametrize("bias_kind", ["col", "full", "bcast"])
 def test_bf16_direct_load_kernel(act, bias_kind):

@@ -140,10 +140,10 @@ def test_fp32_uniform_vs_oracle(hip, shape):
                                          (0, 4400, 1024, 4096)])
 def test_fp32_stream_k_bit_exact(hip, batch, M, K, N):
     """fp32 GEMMs on the stream-K schedule, whose tiles are summed in segments by several
-    workgroups: c1 (672 tiles, 2.625 per CU: one round of whole tiles, then 160 split); 363, 272 and
-    322 tiles with ragged M/N tails and a batch (K of 32 and 33 k-tiles); 12 tiles at K = 9 k-tiles
-    (fewer tiles than CUs); 1024 tiles (two whole rounds, nothing split) and 1120 (two rounds, then
-    96 tiles split over fewer workgroups than are resident).  Integer-valued
+    workgroups: c1 (864 tiles of 96x128, 3.375 per CU: one round of whole tiles, then 352 split);
+    462 (96x128), 272 (128x128) and 414 (96x128) tiles with ragged M/N tails and a batch (K of 32 and
+    33 k-tiles); 12 tiles at K = 9 k-tiles (fewer tiles than CUs); 1024 tiles (two whole rounds,
+    nothing split) and 1120 (two rounds, then 96 tiles split over fewer workgroups than are resident).  Integer-valued
     inputs make every order exact: bit-exact against exact sums, equal to the plain kernel
     (tv_hip_gemm_noalloc takes no workspace, hence no stream-K), and equal on a second call."""
     lead = (batch,) if batch else ()
@@ -165,11 +165,12 @@ def test_fp32_stream_k_bit_exact(hip, batch, M, K, N):
     (0, 2000, 300, 2050, "128x128"), (0, 300, 264, 4096, "64x128"), (0, 4096, 200, 192, "128x64"),
     (8, 1000, 264, 129, "128x64"), (0, 3000, 200, 129, "128x32"), (0, 3000, 4096, 129, "128x32"),
     (0, 8192, 264, 32, "128x32"), (2, 3000, 520, 96, "128x32"), (0, 300, 520, 1000, "32x128"),
-    (3, 90, 136, 500, "32x128"), (0, 300, 4096, 1000, "32x128")])
+    (3, 90, 136, 500, "32x128"), (0, 300, 4096, 1000, "32x128"), (0, 960, 264, 2000, "96x128"),
+    (0, 1340, 4096, 2100, "96x128"), (2, 1300, 520, 700, "96x128"), (3, 1700, 136, 600, "96x128")])
 def test_fp32_tile_choice_exact(hip, batch, M, K, N, tile):
     """fp32 GEMMs that the tile cost rule (padded work over tile rate and CU fill) sends to each of
-    the five fp32 tiles named, with ragged M/N edges, batches, and K = 4096 (the stream-K schedule
-    on 120 and 80 tiles).  Integer-valued inputs make every order exact: bit-exact against exact
+    the six fp32 tiles named, with ragged M/N edges, batches, and K = 4096 (the stream-K schedule
+    on 120, 80 and 238 tiles).  Integer-valued inputs make every order exact: bit-exact against exact
     sums, and equal to the plain kernel (tv_hip_gemm_noalloc: no workspace, no stream-K)."""
     lead = (batch,) if batch else ()
     a = ints(31, lead + (M, K), -3, 3)
@@ -180,6 +181,24 @@ def test_fp32_tile_choice_exact(hip, batch, M, K, N, tile):
     np.testing.assert_array_equal(c, want)
     plain = torch.zeros(lead + (M, N), dtype=torch.float32, device="cuda")
     args = tv.make_args(ta, tb, plain)
+    tv.check(tv.lib().tv_hip_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(plain), c)
+
+
+@pytest.mark.parametrize("M,K,N", [(2592, 520, 1000), (1340, 264, 2100), (960, 4096, 2000)])
+def test_fp32_96_row_tile_k_contiguous_b_exact(hip, M, K, N):
+    """The 96x128 fp32 tile with B stored [N, K] and used transposed (k-contiguous B), ragged and
+    whole row counts, the last on the stream-K schedule (K = 4096): bit-exact on integer-valued
+    inputs, equal to the plain kernel (tv_hip_gemm_noalloc)."""
+    a = ints(41, (M, K), -3, 3)
+    w = ints(42, (N, K), -3, 3)
+    ta, tw = to_torch(a, FLOAT32), to_torch(w, FLOAT32)
+    want = np.matmul(a.astype(np.float64), w.T.astype(np.float64)).astype(np.float32)
+    c = to_storage(hip.gemm(ta, tw.t()))
+    np.testing.assert_array_equal(c, want)
+    plain = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    args = tv.make_args(ta, tw.t(), plain)
     tv.check(tv.lib().tv_hip_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(to_storage(plain), c)
