@@ -86,6 +86,9 @@ public:
     // (TV_HIP_CACHE_LIMIT_MB, default a quarter of the device's memory; 0 turns the cache off):
     // past the cap a released block is freed after a stream synchronisation, as without a cache.
     // When hipMalloc fails the cache is emptied and the allocation tried once more.
+    // Work that a caller queues on another stream with a tensor's data() is outside that order:
+    // it must have completed before the tensor is destroyed (hipFree waited for the whole device;
+    // a cached block goes straight to the next tensor of the context).
     // alloc() returns nullptr for 0 bytes and sets *capacity to the block's size.
     void* alloc(size_t bytes, size_t* capacity);
     void release(void* p, size_t capacity);
