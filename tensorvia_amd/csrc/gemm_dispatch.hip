@@ -72,7 +72,29 @@ int pad_gemm_operands(GemmDesc& d, hipStream_t stream) {
     return rc ? rc : pad_operand(d, false, stream);
 }
 
-int launch_gemm_mfma(const GemmDesc& d, hipStream_t stream, bool may_alloc) {
+// The stride of a dimension of extent 1 (A's rows when M = 1, B's columns when N = 1, either
+// operand's k when K = 1) never steps between two elements a kernel reads, and the caller may pass
+// any value there (torch gives a [K, 1] tensor strides (1, 1)).  The vector loaders size each
+// buffer range from it, as rows x row stride (k-contiguous) or k rows x k stride (m/n-contiguous),
+// so a stride below the row's length cut the one row short, and the elements past the cut read as
+// zeros.  Such a stride is replaced by the row's length rounded up to whole 16-byte chunks; the
+// zero-padded copies (pad_a / pad_b) already have row strides of that kind.
+static GemmDesc with_unit_extent_strides(GemmDesc d) {
+    auto up = [](int64_t x, int64_t v) { return ((x > 1 ? x : 1) + v - 1) / v * v; };
+    const int64_t va = 16 / (int64_t)dtype_size(d.dtype_a), vb = 16 / (int64_t)dtype_size(d.dtype_b);
+    if (!d.pad_a) {
+        if (d.M <= 1) d.sa_m = up(d.K, va);
+        if (d.K <= 1) d.sa_k = up(d.M, va);
+    }
+    if (!d.pad_b) {
+        if (d.N <= 1) d.sb_n = up(d.K, vb);
+        if (d.K <= 1) d.sb_k = up(d.N, vb);
+    }
+    return d;
+}
+
+int launch_gemm_mfma(const GemmDesc& d0, hipStream_t stream, bool may_alloc) {
+    const GemmDesc d = with_unit_extent_strides(d0);
     switch (d.dtype_a) {
         case TV_FLOAT32: return launch_gemm_mfma_f32(d, stream, may_alloc);
         case TV_BFLOAT16: return launch_gemm_mfma_bf16(d, stream, may_alloc);

@@ -204,6 +204,45 @@ def test_fp32_96_row_tile_k_contiguous_b_exact(hip, M, K, N):
     np.testing.assert_array_equal(to_storage(plain), c)
 
 
+@pytest.mark.parametrize("dt", [FLOAT32, BFLOAT16, INT8], ids=["fp32", "bf16", "int8"])
+@pytest.mark.parametrize("case", ["n1", "k1", "m1", "b1_k1_bcast", "b1_n1_at"])
+def test_unit_extent_strides(hip, dt, case):
+    """Operands with a dimension of extent 1 whose stride is smaller than the row it does not step
+    over, as torch lays out [K, 1] or [M, 1] (strides (1, 1)): B = W[K, 1] (N = 1), A[M, 1] @ B[1, N]
+    (K = 1), A[1, K] as a transposed view of [K, 1] storage (M = 1, on the GEMM: B k-contiguous),
+    and the same in 3-d with batch 1.  A loader that sized its buffer range from such a stride cut
+    the row short (the elements past the cut read as zeros).  Integer-valued inputs: bit-exact."""
+    def enc(x):
+        if dt == INT8:
+            return x.astype(np.int8)
+        return half_bits(x.astype(np.float32), dt) if dt == BFLOAT16 else x.astype(np.float32)
+
+    if case == "n1":
+        x, y = ints(51, (300, 708), -3, 3), ints(52, (708, 1), -3, 3)
+        ta, tb = to_torch(enc(x), dt), to_torch(enc(y), dt)
+    elif case == "k1":
+        x, y = ints(53, (256, 1), -3, 3), ints(54, (1, 300), -3, 3)
+        ta, tb = to_torch(enc(x), dt), to_torch(enc(y), dt)
+    elif case == "m1":
+        x, w = ints(55, (708, 1), -3, 3), ints(56, (300, 708), -3, 3)
+        ta = to_torch(enc(x), dt).t()          # [1, 708], strides (1, 1)
+        tb = to_torch(enc(w), dt).t()          # [708, 300], k-contiguous
+        x, y = x.T, w.T
+    elif case == "b1_k1_bcast":
+        x, y = ints(57, (1, 20, 1), -3, 3), ints(58, (1, 3), -3, 3)
+        ta, tb = to_torch(enc(x), dt), to_torch(enc(y), dt)
+    else:
+        xs, y = ints(59, (1, 708, 17), -3, 3), ints(60, (708, 1), -3, 3)
+        ta = to_torch(enc(xs), dt).transpose(-1, -2)  # [1, 17, 708], m-contiguous
+        tb = to_torch(enc(y), dt)[None]              # [1, 708, 1]
+        x, y = np.swapaxes(xs, -1, -2), y[None]
+    s64 = np.matmul(x.astype(np.float64), y.astype(np.float64))
+    want = s64.astype(np.int64).astype(np.int8) if dt == INT8 else enc(s64)
+    c = hip.gemm(ta, tb)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(c), want)
+
+
 def test_fp32_config1_full_size_sampled(hip):
     """c1: fp32 [2592,2048] @ [2048,4096] U[-1,1]: sampled rows/columns against fp64 sums."""
     M, K, N = 2592, 2048, 4096
