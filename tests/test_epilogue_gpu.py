@@ -275,3 +275,33 @@ def test_infinite_bias_gives_the_activation_limits(act, dt, M, K, N):
     inf_cols = np.isinf(bias)
     np.testing.assert_array_equal(c[:, inf_cols], ref[:, inf_cols])  # NaN == NaN here
     assert np.isfinite(c[:, ~inf_cols]).all()
+
+
+def _random_epilogue_cases(n=40, seed=20261205):
+    """Seeded random fused calls: dtype pair, batch, shape (M, N, K log-uniform from 1 to about
+    1500), bias layout, activation and B's layout."""
+    r = np.random.default_rng(seed)
+    pairs = [(tv.FLOAT32, tv.FLOAT32), (tv.BFLOAT16, tv.BFLOAT16), (tv.FLOAT16, tv.FLOAT16), (tv.BFLOAT16, tv.FLOAT32)]
+    out = []
+    while len(out) < n:
+        dt_in, dt_out = pairs[len(out) % 4]
+        M, N, K = (int(np.exp(r.uniform(0, np.log(1500)))) for _ in range(3))
+        batch = int(r.choice([0, 0, 2]))
+        if max(batch, 1) * M * N * K > 4e7:
+            continue
+        kinds = ["col", "full", "none"] + (["colb", "bcast"] if batch else [])
+        out.append((dt_in, dt_out, batch, M, K, N, str(r.choice(kinds)), int(r.choice(list(ACTS))), bool(r.integers(2))))
+    return out
+
+
+RANDOM_EPILOGUE = _random_epilogue_cases()
+
+
+@pytest.mark.parametrize("case", RANDOM_EPILOGUE, ids=[
+    f"{NAME[c[0]]}-{NAME[c[1]]}-b{c[2]}-{c[3]}x{c[5]}x{c[4]}-{c[6]}-{ACT_NAMES[c[7]]}{'-bt' if c[8] else ''}"
+    for c in RANDOM_EPILOGUE])
+def test_random_fused_calls(case):
+    """The fused epilogue on seeded random calls (every kernel family the router picks for them)
+    against the fp64 composition act(A @ B + bias), within the matmul's own bound."""
+    dt_in, dt_out, batch, M, K, N, bias_kind, act, bt = case
+    run_case(dt_in, dt_out, batch, M, K, N, bias_kind, act, bt=bt, seed=7 * M + 11 * N + 13 * K)

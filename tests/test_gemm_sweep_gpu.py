@@ -8,8 +8,12 @@ row copies of misaligned operands and the element-gather loader.
 Inputs are integers in [-3, 3], so every accumulation order gives the same fp32 / int32 sum: fp32
 outputs must equal the exact sum, half outputs the exact sum rounded once, int8 outputs its low
 byte (the reference CPU backend's wrap-around result), bit for bit.  The expected values come from
-numpy's float64 matmul, exact here (|sum| <= 9 K < 2^24).
+numpy's float64 matmul, exact here (|sum| <= 9 K < 2^24).  Each call also runs through
+tv_hip_gemm_noalloc, which must give the same sums without a workspace (or decline with
+TV_E_SCRATCH when the GEMV's partials exceed its static scratch).
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -82,6 +86,17 @@ def test_random_call_exact(hip, case):
     x = rng.uniform_int(seed, int(np.prod(lead + (M, K))), -3, 3).reshape(lead + (M, K))
     yshape = (K, N) if bcast or not batch else lead + (K, N)
     y = rng.uniform_int(seed + 1, int(np.prod(yshape)), -3, 3).reshape(yshape)
-    c = hip.gemm(_dev(x, dt, at), _dev(y, dt, bt))
+    ta, tb = _dev(x, dt, at), _dev(y, dt, bt)
+    c = hip.gemm(ta, tb)
     torch.cuda.synchronize()
-    np.testing.assert_array_equal(to_storage(c), _expect(x, y, dt), err_msg=_name(case))
+    want = _expect(x, y, dt)
+    np.testing.assert_array_equal(to_storage(c), want, err_msg=_name(case))
+    # tv_hip_gemm_noalloc on the same call: no workspace (no stream-K split, no padded copies, the
+    # GEMV's partials in the static scratch), the same exact sums.
+    plain = torch.full_like(c, 7)
+    args = hip.make_args(ta, tb, plain)
+    rc = hip.lib().tv_hip_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc in (hip.TV_OK, hip.TV_E_SCRATCH), hip.strerror(rc)
+    torch.cuda.synchronize()
+    if rc == hip.TV_OK:
+        np.testing.assert_array_equal(to_storage(plain), want, err_msg=_name(case) + " (no-allocation entry)")
