@@ -87,3 +87,45 @@ def test_element_general_permute():
 def test_misaligned_source_falls_back():
     # a 16-byte-row view whose base is 2 bytes off 16-byte alignment
     run_case(4 * 64 + 1, 2, [4, 64], [64, 1], 1, seed=51)
+
+
+def _random_views(n=60, seed=20261206):
+    """Seeded random views of a random base tensor: rank 1 to 4, a random permutation of the base's
+    axes, a random slice (start, stop, step 1 to 3) of each, sometimes one axis broadcast with
+    stride 0; element sizes 1, 2, 4 and 8 bytes."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        es = int(r.choice([1, 2, 4, 8]))
+        rank = int(r.integers(1, 5))
+        base = [int(np.exp(r.uniform(0, np.log(300 if rank <= 2 else 40)))) for _ in range(rank)]
+        bstr = [int(np.prod(base[d + 1:])) for d in range(rank)]  # row-major element strides
+        shape, strides, offset = [], [], 0
+        for d in range(rank):
+            step = int(r.choice([1, 1, 1, 2, 3]))
+            lo = int(r.integers(0, base[d]))
+            hi = int(r.integers(lo + 1, base[d] + 1))
+            shape.append(len(range(lo, hi, step)))
+            strides.append(bstr[d] * step)
+            offset += lo * bstr[d]
+        perm = [int(p) for p in r.permutation(rank)]
+        shape, strides = [shape[p] for p in perm], [strides[p] for p in perm]
+        if rank > 1 and r.integers(4) == 0:
+            d = int(r.integers(rank))
+            shape[d], strides[d] = int(r.integers(1, 6)), 0
+        if int(np.prod(shape)) * es > (64 << 20):
+            continue
+        out.append((int(np.prod(base)), es, shape, strides, offset))
+    return out
+
+
+RANDOM_VIEWS = _random_views()
+
+
+@pytest.mark.parametrize("case", RANDOM_VIEWS, ids=[f"es{c[1]}-{'x'.join(map(str, c[2]))}-s{'_'.join(map(str, c[3]))}"
+                                                    for c in RANDOM_VIEWS])
+def test_random_views(case):
+    """clone_as_contiguous of seeded random views (permuted, sliced with steps, broadcast):
+    bit-exact against the same view gathered on the host."""
+    storage, es, shape, strides, offset = case
+    run_case(storage, es, shape, strides, offset, seed=len(shape) * 1000 + offset % 997)
