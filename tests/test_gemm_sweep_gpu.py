@@ -45,8 +45,10 @@ def _cases(n, seed, mn, k, max_macs):
 
 
 # Any size from 1 (GEMVs, small K, tiny tiles), then tile-sized shapes (128x128 / 256x256 tiles,
-# stream-K and chained schedules, the fp32 tile choice).
-CASES = _cases(48, 20261202, (1, 3000), (1, 3000), 1.5e8) + _cases(24, 20261203, (200, 2600), (16, 2048), 4e8)
+# stream-K and chained schedules, the fp32 tile choice), then shapes of hundreds of tiles (the
+# boundaries between one round of tiles, several, and the schedules that split them).
+CASES = (_cases(48, 20261202, (1, 3000), (1, 3000), 1.5e8) + _cases(24, 20261203, (200, 2600), (16, 2048), 4e8)
+         + _cases(16, 20261207, (1000, 4500), (48, 4096), 4e9))
 
 
 def _enc(x, dt):
