@@ -38,6 +38,27 @@ CASES = [
     ("i32_simt", INT32, INT32, "contig", 0, 50, 70, 40, -50, 50, 23, 24),
     ("i32_f32_mixed", INT32, FLOAT32, "contig", 0, 33, 65, 17, -50, 50, 25, 26),
 ]
+
+
+def _random_cases(n=24, seed=20261208):
+    """Seeded random ops::Mul calls through the C++ API: dtype, layout (contiguous, B broadcast,
+    B or A transposed, sliced views with offsets), batch and shape (M, N, K log-uniform)."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        dt = [INT8, FLOAT32, BFLOAT16, FLOAT16][len(out) % 4]
+        layout = str(r.choice(["contig", "bcast", "bt", "at", "slice"]))
+        batch = int(r.choice([1, 2, 3])) if layout == "bcast" else int(r.choice([0, 0, 2]))
+        M, K, N = (int(np.exp(r.uniform(0, np.log(1200)))) for _ in range(3))
+        if max(batch, 1) * M * N * K > 5e7:
+            continue
+        lo, hi = (-128, 127) if dt == INT8 else (-1, 1)
+        i = len(out)
+        out.append((f"rand{i}_{NAMES[dt]}_{layout}", dt, dt, layout, batch, M, K, N, lo, hi, 100 + 2 * i, 101 + 2 * i))
+    return out
+
+
+CASES += _random_cases()
 # K = 0 cannot reach ops::Mul: a tensor with a zero-sized dimension is rejected when it is built
 # (calc_numel, reference include/core/type_traits.h:296; tests/cpp/host_api_test.cpp checks it).
 # The C-ABI serves K = 0 (tests/test_edge_gpu.py).
