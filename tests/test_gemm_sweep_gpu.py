@@ -26,13 +26,13 @@ pytestmark = pytest.mark.gpu
 DTYPES = [FLOAT32, BFLOAT16, FLOAT16, INT8]
 
 
-def _cases(n, seed, mn, k, max_macs):
+def _cases(n, seed, mn, k, max_macs, dtypes=DTYPES):
     """n calls with M, N log-uniform in [mn[0], mn[1]] and K in [k[0], k[1]], at most max_macs
     multiply-adds each (keeps the host-side reference and the sweep to seconds)."""
     r = np.random.default_rng(seed)
     out = []
     while len(out) < n:
-        dt = DTYPES[len(out) % 4]
+        dt = dtypes[len(out) % len(dtypes)]
         M, N = (int(np.exp(r.uniform(np.log(mn[0]), np.log(mn[1])))) for _ in range(2))
         K = int(np.exp(r.uniform(np.log(k[0]), np.log(k[1]))))
         batch = int(r.choice([0, 0, 1, 3]))
@@ -46,9 +46,12 @@ def _cases(n, seed, mn, k, max_macs):
 
 # Any size from 1 (GEMVs, small K, tiny tiles), then tile-sized shapes (128x128 / 256x256 tiles,
 # stream-K and chained schedules, the fp32 tile choice), then shapes of hundreds of tiles (the
-# boundaries between one round of tiles, several, and the schedules that split them).
+# boundaries between one round of tiles, several, and the schedules that split them), then long K
+# (the GEMVs' K slices and x staging, the split-K schedules; fp16 is left out there, since sums of
+# that many terms leave its range).
 CASES = (_cases(48, 20261202, (1, 3000), (1, 3000), 1.5e8) + _cases(24, 20261203, (200, 2600), (16, 2048), 4e8)
-         + _cases(16, 20261207, (1000, 4500), (48, 4096), 4e9))
+         + _cases(16, 20261207, (1000, 4500), (48, 4096), 4e9)
+         + _cases(12, 20261209, (1, 600), (4000, 120000), 4e8, [FLOAT32, BFLOAT16, INT8]))
 
 
 def _enc(x, dt):
