@@ -7,7 +7,8 @@ row copies of misaligned operands and the element-gather loader.
 
 Inputs are integers in [-3, 3], so every accumulation order gives the same fp32 / int32 sum: fp32
 outputs must equal the exact sum, half outputs the exact sum rounded once, int8 outputs its low
-byte (the reference CPU backend's wrap-around result), bit for bit.  The expected values come from
+byte (the reference CPU backend's wrap-around result), bit for bit; every third int8 or half call
+asks for the widened int32 / fp32 output, which must hold the exact sum.  The expected values come from
 numpy's float64 matmul, exact here (|sum| <= 9 K < 2^24).  Each call also runs through
 tv_hip_gemm_noalloc, which must give the same sums without a workspace (or decline with
 TV_E_SCRATCH when the GEMV's partials exceed its static scratch).
@@ -19,7 +20,7 @@ import pytest
 import torch
 
 from tensorvia_amd import rng
-from tests.util import BFLOAT16, FLOAT16, FLOAT32, INT8, to_storage, to_torch
+from tests.util import BFLOAT16, FLOAT16, FLOAT32, INT8, INT32, to_storage, to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -69,18 +70,25 @@ def _dev(x, dt, transposed):
     return to_torch(np.ascontiguousarray(_enc(x, dt)), dt)
 
 
-def _expect(x, y, dt):
+def _expect(x, y, dt, wide):
     s = np.matmul(x.astype(np.float64), y.astype(np.float64))
     if dt == INT8:
-        return s.astype(np.int64).astype(np.int8)  # low byte of the exact sum (two's complement)
-    return _enc(s.astype(np.float32), dt)
+        # the full int32 sum, or its low byte (two's complement)
+        return s.astype(np.int32) if wide else s.astype(np.int64).astype(np.int8)
+    return s.astype(np.float32) if wide else _enc(s.astype(np.float32), dt)
+
+
+def _wide(case):
+    """Every third int8 / half call asks for the widened output (int32 / fp32) the C-ABI offers."""
+    dt, batch, M, N, K = case[:5]
+    return dt != FLOAT32 and (M + N + K) % 3 == 0
 
 
 def _name(c):
     dt, batch, M, N, K, bcast, at, bt = c
     nm = {FLOAT32: "fp32", BFLOAT16: "bf16", FLOAT16: "fp16", INT8: "int8"}[dt]
     lead = f"b{batch}{'bc' if bcast else ''}-" if batch else ""
-    return f"{nm}-{lead}{M}x{N}x{K}-{'AT' if at else 'A'}{'BT' if bt else 'B'}"
+    return f"{nm}-{lead}{M}x{N}x{K}-{'AT' if at else 'A'}{'BT' if bt else 'B'}" + ("-wide" if _wide(c) else "")
 
 
 @pytest.mark.parametrize("case", CASES, ids=[_name(c) for c in CASES])
@@ -92,9 +100,10 @@ def test_random_call_exact(hip, case):
     yshape = (K, N) if bcast or not batch else lead + (K, N)
     y = rng.uniform_int(seed + 1, int(np.prod(yshape)), -3, 3).reshape(yshape)
     ta, tb = _dev(x, dt, at), _dev(y, dt, bt)
-    c = hip.gemm(ta, tb)
+    wide = _wide(case)
+    c = hip.gemm(ta, tb, out_dtype=(INT32 if dt == INT8 else FLOAT32) if wide else None)
     torch.cuda.synchronize()
-    want = _expect(x, y, dt)
+    want = _expect(x, y, dt, wide)
     np.testing.assert_array_equal(to_storage(c), want, err_msg=_name(case))
     # tv_hip_gemm_noalloc on the same call: no workspace (no stream-K split, no padded copies, the
     # GEMV's partials in the static scratch), the same exact sums.
