@@ -630,6 +630,56 @@ def test_simt_pairs_vs_oracle(hip, pair, shape):
         np.testing.assert_array_equal(got, ref)
 
 
+def _simt_cases(n=40, seed=20261210):
+    """Seeded random calls of the dtype pairs without matrix cores (every pair of the eight dtypes
+    but int8, bf16, fp16 and fp32 with themselves): shape up to 200 a side, each operand row-major
+    or a transposed view, sometimes batched."""
+    r = np.random.default_rng(seed)
+    mfma = {(0, 0), (4, 4), (5, 5), (6, 6)}
+    pairs = [(a, b) for a in range(8) for b in range(8) if (a, b) not in mfma]
+    out = []
+    for i in range(n):
+        da, db = pairs[int(r.integers(len(pairs)))]
+        M, K, N = (int(np.exp(r.uniform(0, np.log(200)))) for _ in range(3))
+        out.append((da, db, int(r.choice([0, 0, 2])), M, K, N, bool(r.integers(2)), bool(r.integers(2))))
+    return out
+
+
+SIMT_CASES = _simt_cases()
+
+
+@pytest.mark.parametrize("case", SIMT_CASES, ids=[f"{c[0]}x{c[1]}-b{c[2]}-{c[3]}x{c[4]}x{c[5]}{'-at' if c[6] else ''}"
+                                                  f"{'-bt' if c[7] else ''}" for c in SIMT_CASES])
+def test_simt_random_pairs_exact(hip, case):
+    """The SIMT kernel on seeded random dtype pairs, shapes, batches and transposed views, with
+    integer inputs in [-50, 50] (exact in every dtype, and every sum exact in the accumulator types):
+    bit-exact against the oracle's MulImpl<CPU>, in the CPU backend's result dtype."""
+    import oracle
+    da, db, batch, M, K, N, at, bt = case
+    lead = (batch,) if batch else ()
+    seed = 3 * M + 5 * K + 7 * N + da * 11 + db
+    a = rng.uniform_int(seed, int(np.prod(lead + (M, K))), -50, 50).reshape(lead + (M, K))
+    b = rng.uniform_int(seed + 1, int(np.prod(lead + (K, N))), -50, 50).reshape(lead + (K, N))
+
+    def enc(x, dt):
+        if dt == BFLOAT16:
+            return rng.f32_to_bf16_bits(x.astype(np.float32))
+        if dt == FLOAT16:
+            return rng.f32_to_f16_bits(x.astype(np.float32))
+        return x.astype(orc.NP[dt])
+
+    def dev(x, dt, t):
+        if t:
+            return to_torch(np.ascontiguousarray(np.swapaxes(enc(x, dt), -1, -2)), dt).transpose(-1, -2)
+        return to_torch(np.ascontiguousarray(enc(x, dt)), dt)
+
+    ea, eb = enc(a, da), enc(b, db)
+    ref = np.stack([oracle.mul(ea[i], da, eb[i], db) for i in range(batch)]) if batch else oracle.mul(ea, da, eb, db)
+    c = hip.gemm(dev(a, da, at), dev(b, db, bt), out_dtype=oracle.result_type(da, db))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(c), ref)
+
+
 def test_rejects_bad_output_dtype(hip):
     a = torch.ones((4, 4), dtype=torch.int8, device="cuda")
     with pytest.raises(hip.TensorviaHipError):
