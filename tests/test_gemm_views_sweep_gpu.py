@@ -3,7 +3,8 @@
 transposed view, a sub-block of a larger tensor (offset and row stride), every other column (a
 stride of 2 along the contiguous dimension), a row or column expanded with stride 0, and, with a
 batch, a batch expanded with stride 0; B may be one matrix broadcast over A's batch.  C is a fresh
-tensor or the first N columns of wider rows, whose padding must come back untouched.
+tensor or N columns of wider rows, starting at column 0, 1 or 2 (an unaligned start), and the
+columns around it must come back untouched.
 
 Integer inputs in [-3, 3] make every accumulation order exact: fp32 outputs equal the exact sum,
 half outputs the exact sum rounded once, int8 outputs its low byte, bit for bit.
@@ -105,12 +106,15 @@ def test_random_views_exact(hip, case):
         tx = tx.expand(batch, M, K)
         x = np.broadcast_to(x, lead + (M, K))
     cshape = lead + (M, N)
+    coff = (M + N) % 3 if cpad else 0  # C's first column inside the wider rows: an unaligned start
     wide = torch.full(lead + (M, N + cpad), 77, dtype=TORCH_DT[dt], device="cuda")
-    c = wide[..., :N]
+    c = wide[..., coff:coff + N] if coff + N <= N + cpad else wide[..., :N]
+    coff = coff if coff + N <= N + cpad else 0
     hip.gemm(tx, ty, out=c)
     torch.cuda.synchronize()
     s = np.matmul(x.astype(np.float64), y.astype(np.float64))
     want = s.astype(np.int64).astype(np.int8) if dt == INT8 else _enc(s.astype(np.float32), dt)
     np.testing.assert_array_equal(to_storage(c.contiguous()).reshape(cshape), want, err_msg=_name(case))
     if cpad:
-        assert bool((wide[..., N:] == 77).all()), f"{_name(case)}: wrote past column N"
+        assert bool((wide[..., :coff] == 77).all()), f"{_name(case)}: wrote before C's first column"
+        assert bool((wide[..., coff + N:] == 77).all()), f"{_name(case)}: wrote past C's last column"
