@@ -81,13 +81,18 @@ enum tv_dtype {
 enum tv_status {
     TV_OK = 0,
     TV_E_NULL = -1,        /* a required pointer is NULL */
-    TV_E_SHAPE = -2,       /* batch/M/N/K negative or a size overflows the kernels' index range */
+    TV_E_SHAPE = -2,       /* batch/M/N/K negative or above TV_MAX_EXTENT, or a size overflows the kernels' index range */
     TV_E_DTYPE = -3,       /* dtype value out of range or output dtype not allowed for the inputs */
     TV_E_UNSUPPORTED = -4, /* valid request that this entry point does not serve (e.g. gemv with M > 8) */
     TV_E_INJECTED = -5,    /* returned by the fault-injection hook (tests only) */
     TV_E_NOMEM = -6,       /* workspace allocation failed */
     TV_E_SCRATCH = -7      /* tv_hip_gemm_noalloc: the call needs more split-K scratch than the static buffer holds */
 };
+
+/* Largest batch, M, N or K the GEMM entry points accept: 2^31 - 2^20 - 1.  Tile, k-tile and slice
+ * counts are 32-bit; the margin keeps their rounded-up sums in range.  Operands, outputs and their
+ * strides may span any number of bytes: every address is formed in 64 bits. */
+#define TV_MAX_EXTENT 2146435071
 
 typedef struct tv_gemm_args {
     int32_t dtype_a, dtype_b, dtype_c; /* enum tv_dtype */

@@ -57,6 +57,7 @@ class TvEpilogue(ctypes.Structure):
 
 
 TV_MAX_DIMS = 8
+TV_MAX_EXTENT = (1 << 31) - (1 << 20) - 1  # largest batch / M / N / K of the GEMM entry points
 
 
 class TvRepackArgs(ctypes.Structure):

@@ -66,7 +66,10 @@ int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
     for (int dt : {a->dtype_a, a->dtype_b, a->dtype_c})
         if (dt < TV_INT8 || dt > TV_FLOAT64) return TV_E_DTYPE;
     if (a->batch < 0 || a->M < 0 || a->N < 0 || a->K < 0) return TV_E_SHAPE;
-    const int64_t lim = 0x7FFFFFFF;
+    // The launchers count tiles, k-tiles and K slices in 32-bit arithmetic from these sizes (tile
+    // rows rounded up, the k offset two k-tiles ahead of the last one): staying 2^20 below INT32_MAX
+    // keeps every such sum in range.
+    const int64_t lim = TV_MAX_EXTENT;
     if (a->batch > lim || a->M > lim || a->N > lim || a->K > lim) return TV_E_SHAPE;
     if (!mfma_pair(a) && a->dtype_c != cpu_result_type(a->dtype_a, a->dtype_b)) return TV_E_DTYPE;
     const bool empty = a->batch == 0 || a->M == 0 || a->N == 0;

@@ -38,6 +38,8 @@ def test_abi_version_matches_header():
     text = (ROOT / "include" / "tensorvia_hip.h").read_text()
     v = int(re.search(r"#define TV_HIP_ABI_VERSION (\d+)", text).group(1))
     assert tv.lib().tv_hip_abi_version() == v
+    ext = int(re.search(r"#define TV_MAX_EXTENT (\d+)", text).group(1))
+    assert ext == tv.TV_MAX_EXTENT == 2**31 - 2**20 - 1
 
 
 @pytest.mark.parametrize("struct,cname", [("TvGemmArgs", "tv_gemm_args"), ("TvRepackArgs", "tv_repack_args"),
@@ -80,6 +82,11 @@ def test_rejections(fn):
     assert _call(fn, _args(dtype_a=tv.BFLOAT16, dtype_b=tv.BFLOAT16, dtype_c=tv.FLOAT16)) == tv.TV_E_DTYPE
     assert _call(fn, _args(M=-1)) == tv.TV_E_SHAPE
     assert _call(fn, _args(K=1 << 40)) == tv.TV_E_SHAPE
+    # Each size is accepted up to TV_MAX_EXTENT (2^31 - 2^20 - 1): one past it is rejected; at it the
+    # call passes the size check and stops at the missing output pointer.
+    for dim in ("batch", "M", "N", "K"):
+        assert _call(fn, _args(**{dim: tv.TV_MAX_EXTENT + 1})) == tv.TV_E_SHAPE, dim
+        assert _call(fn, _args(**{dim: tv.TV_MAX_EXTENT}, C=None)) == tv.TV_E_NULL, dim
     assert _call(fn, _args(C=None)) == tv.TV_E_NULL
     assert _call(fn, _args(A=None)) == tv.TV_E_NULL
     assert _call(fn, _args(flags=1)) == tv.TV_E_UNSUPPORTED
