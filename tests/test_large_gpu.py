@@ -4,7 +4,8 @@ kernels form is a 64-bit base (per batch, tile, k-tile or K slice) plus a 32-bit
 range checked on the host; these calls put the bases past 2^32 for each kernel family: the
 256x256 direct-load tiles and the chained schedule (bf16, fp16, int8), the fp32 tiles, the
 row-synchronous small-K kernel over batches, both GEMV layouts, the SIMT path, the transpose,
-the cast and the seeded generator.
+the cast and the seeded generator; and through the C++ API, a host round trip and ops::Mul past
+4 GiB (tests/cpp/large_driver.cpp).
 
 Checks, all exact:
 * sampled rows or columns (always including the first and the last) against numpy's float64 or
@@ -16,6 +17,7 @@ Inputs are integers in {-1, 0, 1} (or [-3, 3] for int8), so every sum is exact i
 (|sum| <= 256 in bf16, <= 2048 in fp16, below 2^24 in fp32) and every accumulation order agrees.
 """
 import ctypes
+import subprocess
 
 import numpy as np
 import pytest
@@ -271,3 +273,15 @@ def test_random_and_fill_past_2g_elements(hip):
     tv.check(tv.lib().tv_hip_fill(ctypes.c_void_p(f.data_ptr()), tv.FLOAT32, m, 2.5, s))
     torch.cuda.synchronize()
     assert bool((f == 2.5).all())
+
+
+def test_cpp_api_past_4gib(hip):
+    """The C++ API end to end: a host -> device -> host round trip of 4 GiB + 12,345 bytes through
+    the pinned staging chunks, and ops::Mul of a 5.4 GB int8 A made by the device ops::Random,
+    sampled rows on either side of A's byte offset 2^32 equal to the low byte of the exact sums
+    (tests/cpp/large_driver.cpp, in a child process)."""
+    from tests.cpp import build as cpp
+    r = subprocess.run([str(cpp.binary("large_driver"))], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
+    assert "ok round_trip 4294979641 bytes" in r.stdout, r.stdout
+    assert "ok mul int8 [131072,40960]@[40960,256]: 12 sampled rows" in r.stdout, r.stdout
