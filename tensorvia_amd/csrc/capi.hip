@@ -27,8 +27,6 @@ bool enter_call(int* code) {
     return false;
 }
 
-bool is_float_dt(int dt) { return dt == TV_BFLOAT16 || dt == TV_FLOAT16 || dt == TV_FLOAT32 || dt == TV_FLOAT64; }
-
 // Output dtypes each input pair may produce.  For the matrix-core dtypes the GPU-backend result
 // type (compute_type(a, b), reference include/core/type_traits.h:270-287) and the widened CPU
 // backend result (src/backend/cpu/mul.cpp:110-112) are both served; other pairs produce exactly
@@ -87,7 +85,6 @@ int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
     d->sbias_b = d->sbias_m = d->sbias_n = 0;
     d->bias_bytes = 0;
     d->act = TV_ACT_NONE;
-    (void)is_float_dt;
     return TV_OK;
 }
 
