@@ -78,3 +78,37 @@ def test_noalloc_rejects_a_split_beyond_the_static_scratch(hip):
     assert "static" in tv.strerror(tv.TV_E_SCRATCH)
     tv.check(tv.lib().tv_hip_gemm(ctypes.byref(args), sh))
     torch.cuda.synchronize()
+
+
+def test_noalloc_in_a_captured_graph(hip):
+    """The callers the entry point is for, under HIP graph capture: a graph records two
+    tv_hip_gemm_noalloc calls (bf16 x[8, 4096] @ W[4096, 11008] on the split-K GEMV, whose partials
+    and counters live in the static array, then an int8 GEMM) and is replayed five times, with eager
+    work in between (fills of the outputs, a smaller eager no-alloc call that reuses the array,
+    synchronisations); every replay equals the eager tv_hip_gemm results bit for bit."""
+    L = tv.lib()
+    a1, b1 = _operands(BFLOAT16, (8, 4096), (4096, 11008), 90)
+    a2, b2 = _operands(INT8, (300, 512), (512, 640), 92)
+    x3, w3 = _operands(BFLOAT16, (1, 1024), (1024, 2048), 94)
+    want1, want2 = _call("tv_hip_gemm", a1, b1), _call("tv_hip_gemm", a2, b2)
+    want3 = _call("tv_hip_gemm", x3, w3)
+    # Eager first calls: the static array's set-up and the per-shape plans happen outside the capture.
+    np.testing.assert_array_equal(_call("tv_hip_gemm_noalloc", a1, b1), want1)
+    np.testing.assert_array_equal(_call("tv_hip_gemm_noalloc", a2, b2), want2)
+    c1 = torch.zeros((8, 11008), dtype=torch.bfloat16, device="cuda")
+    c2 = torch.zeros((300, 640), dtype=torch.int8, device="cuda")
+    args1, args2 = tv.make_args(a1, b1, c1), tv.make_args(a2, b2, c2)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        tv.check(L.tv_hip_gemm_noalloc(ctypes.byref(args1), sh))
+        tv.check(L.tv_hip_gemm_noalloc(ctypes.byref(args2), sh))
+    for r in range(5):
+        c1.fill_(3.0)
+        c2.fill_(3)
+        np.testing.assert_array_equal(_call("tv_hip_gemm_noalloc", x3, w3), want3, err_msg=f"eager call before replay {r}")
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_storage(c1), want1, err_msg=f"replay {r}: GEMV")
+        np.testing.assert_array_equal(to_storage(c2), want2, err_msg=f"replay {r}: GEMM")
