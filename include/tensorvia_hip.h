@@ -153,7 +153,9 @@ int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_st
  * partials), whose fp32 and 16-bit results can then differ from tv_hip_gemm's in the last bits.
  * The first call on a GPU looks the array up (hipGetSymbolAddress) and clears its counters with a
  * kernel on hip_stream.  All calls on one GPU share its array: calls that overlap on one GPU (on
- * different streams, or from different threads) race and must be serialised by the caller. */
+ * different streams, or from different threads) race and must be serialised by the caller.  Under
+ * graph capture, make a shape's first call outside the capture (it sets up the array and the
+ * shape's launch plan); the captured calls then replay exactly. */
 int tv_hip_gemm_noalloc(const tv_gemm_args* args, void* hip_stream);
 
 /* Skinny-M (M <= 8) matrix-vector path, HBM-streaming.  W N-contiguous (x @ W, W[K, N] row-major):
