@@ -9,7 +9,7 @@ from tensorvia_amd.host import build_host as bh
 
 HERE = Path(__file__).resolve().parent
 BIN = HERE / "bin"
-PROGRAMS = ["host_api_test", "mul_driver", "init_driver", "copy_driver", "large_driver"]
+PROGRAMS = ["host_api_test", "mul_driver", "init_driver", "copy_driver", "large_driver", "threads_driver"]
 
 
 def build(verbose: bool = False) -> None:

@@ -5,7 +5,11 @@ atomics; calls on different streams must neither share a buffer nor race on the 
 thread issues every workspace user in turn, without synchronising between calls, so kernels of the
 same kind run on several streams at once; every result must then equal the exact sum of its
 integer inputs (its low byte for int8 outputs, rounded once for bf16), bit for bit.
+
+The same through the C++ API: tests/cpp/threads_driver.cpp runs ops::Random -> ops::Mul -> to_host()
+from four threads that share the HIP context (its stream, block cache and pinned staging).
 """
+import subprocess
 import threading
 
 import numpy as np
@@ -76,3 +80,14 @@ def test_threads_on_separate_streams_exact(hip):
         assert len(results[t]) == ITERS * len(CASES)
         for n, (k, c) in enumerate(results[t]):
             np.testing.assert_array_equal(to_storage(c), wants[k], err_msg=f"thread {t} call {n} ({CASES[k][0]})")
+
+
+def test_cpp_api_from_four_threads(hip):
+    """Four threads share the C++ API's HIP context, 12 rounds each (int8, bf16, fp32 GEMV, int8
+    GEMV): every round's bytes equal the thread's first round, and the int8 threads' sampled rows
+    equal the low byte of the exact sums (tests/cpp/threads_driver.cpp, in a child process)."""
+    from tests.cpp import build as cpp
+    r = subprocess.run([str(cpp.binary("threads_driver"))], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
+    for t in range(4):
+        assert f"ok thread {t}: 12 rounds" in r.stdout, r.stdout
