@@ -36,7 +36,9 @@ def _int_operands(dt, shape_a, shape_b, seed, lo, hi):
 def _exact(dt, a, b):
     """Exact product of integer-valued operands, in the output's storage."""
     if dt == INT8:
-        return (a.astype(np.int64) @ b.astype(np.int64)).astype(np.int8)  # low byte (two's complement)
+        # float64 products and sums of int8 values are exact here (|sum| <= 127^2 K < 2^53); then the
+        # low byte (two's complement)
+        return (a.astype(np.float64) @ b.astype(np.float64)).astype(np.int64).astype(np.int8)
     fa, fb = to_f32(a, dt).astype(np.float64), to_f32(b, dt).astype(np.float64)
     c = (fa @ fb).astype(np.float32)
     return rng.f32_to_bf16_bits(c) if dt == BFLOAT16 else c
@@ -123,3 +125,38 @@ def test_noalloc_on_padded_skinny_float_call(hip):
     assert_half_close(f2, ref, bound, 4096)
     ulp = np.spacing(np.maximum(np.abs(f1), np.abs(f2)).astype(np.float32)) * 65536  # bf16 ulp: 2^16 fp32 ulps
     assert (np.abs(f1 - f2) <= 2 * ulp).all()
+
+
+def test_workspace_users_captured_after_a_warm_up(hip):
+    """tv_hip_gemm under HIP graph capture: once a stream's workspace has grown on an eager call of
+    each shape, the same calls on that stream allocate and synchronise nothing, so a graph can
+    record them.  The workspace users of CASES are captured on one stream and replayed five times,
+    with eager fills of the outputs in between; every replay is exact."""
+    L = tv.lib()
+    s = torch.cuda.Stream()
+    calls = []
+    for i, (name, dt, sa, sb, r) in enumerate(CASES):
+        a, b = _int_operands(dt, sa, sb, 970 + i, -r, r)
+        ta, tb = to_torch(a, dt), to_torch(b, dt)
+        tc = torch.zeros(tuple(ta.shape[:-1]) + (tb.shape[-1],), dtype=ta.dtype, device="cuda")
+        # the operands stay referenced here: the descriptor holds their raw pointers
+        calls.append((name, _exact(dt, a, b), (ta, tb), tc, tv.make_args(ta, tb, tc)))
+    torch.cuda.synchronize()
+    sh = ctypes.c_void_p(s.cuda_stream)
+    for name, want, ops, tc, args in calls:  # the warm-up: grows the stream's workspace
+        assert L.tv_hip_gemm(ctypes.byref(args), sh) == tv.TV_OK, name
+    s.synchronize()
+    for name, want, ops, tc, args in calls:
+        np.testing.assert_array_equal(to_storage(tc), want, err_msg=f"{name}: eager")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for name, want, ops, tc, args in calls:
+            tv.check(L.tv_hip_gemm(ctypes.byref(args), sh))
+    for rep in range(5):
+        for name, want, ops, tc, args in calls:
+            tc.fill_(5)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for name, want, ops, tc, args in calls:
+            np.testing.assert_array_equal(to_storage(tc), want, err_msg=f"{name}: replay {rep}")
