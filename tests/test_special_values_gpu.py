@@ -125,3 +125,38 @@ def test_inf_and_nan_operands_simt(hip):
     c = hip.gemm(ta, tb)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(to_storage(c), want)
+
+
+# (name, dtype, batch, M, K, N, B stored transposed, output dtype or None, entry, scale exponent)
+DENORMAL_CASES = [
+    ("fp32_tiles", FLOAT32, 0, 300, 512, 200, False, None, "gemm", -70),
+    ("fp32_stream_k", FLOAT32, 0, 64, 8192, 64, False, None, "gemm", -70),
+    ("fp32_gemv_dot", FLOAT32, 0, 2, 4096, 3000, False, None, "gemm", -70),
+    ("bf16_256_tiles_fp32_out", BFLOAT16, 0, 512, 512, 512, False, FLOAT32, "gemm", -70),
+    ("bf16_256_tiles_bf16_out", BFLOAT16, 0, 512, 512, 512, False, None, "gemm", -67),
+    ("bf16_gemv_m1", BFLOAT16, 0, 1, 4096, 4096, False, FLOAT32, "gemv", -70),
+    ("bf16_gemv_m8_k_contiguous_w", BFLOAT16, 0, 8, 4096, 2048, True, FLOAT32, "gemv", -70),
+    ("fp16_small_k_fp16_out", FLOAT16, 16, 1024, 64, 1024, True, None, "gemm", -12),
+]
+
+
+@pytest.mark.parametrize("case", DENORMAL_CASES, ids=[c[0] for c in DENORMAL_CASES])
+def test_denormal_products_and_sums_exact(hip, case):
+    """Operands are small integers times 2^e, normal numbers whose products and sums lie in the
+    output's denormal range (fp32: multiples of 2^-140 against a smallest normal of 2^-126; bf16
+    output: multiples of 2^-134, rounded to bf16's denormal step of 2^-133; fp16: multiples of 2^-24
+    against 2^-14).  Those sums are exact in fp32, so nothing may flush
+    them to zero: fp32 outputs equal the exact sums, half outputs the exact sums rounded once, as
+    the reference CPU backend's IEEE arithmetic gives them."""
+    name, dt, batch, M, K, N, bt, out_dt, entry, e = case
+    lead = (batch,) if batch else ()
+    x = rng.uniform_int(3 * M + K, int(np.prod(lead + (M, K))), -3, 3).reshape(lead + (M, K)) * 2.0 ** e
+    y = rng.uniform_int(5 * N + K, int(np.prod(lead + (K, N))), -3, 3).reshape(lead + (K, N)) * 2.0 ** e
+    want = np.matmul(x, y)
+    c = (hip.gemv if entry == "gemv" else hip.gemm)(_dev(x, dt, False), _dev(y, dt, bt), out_dtype=out_dt)
+    torch.cuda.synchronize()
+    cdt = dt if out_dt is None else out_dt
+    expect = to_f32(_enc(want, cdt), cdt)
+    tiny = np.finfo(np.float16 if cdt == FLOAT16 else np.float32).tiny
+    assert ((expect != 0) & (np.abs(expect) < tiny)).mean() > 0.5, name  # mostly denormal outputs
+    np.testing.assert_array_equal(to_f32(to_storage(c), cdt), expect, err_msg=name)
