@@ -27,6 +27,7 @@ import argparse
 import ctypes
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -434,6 +435,103 @@ def run_ops_mul(iters: int = 100) -> dict:
     return out
 
 
+def _smi_sample():
+    """(board power W, mean shader clock MHz) from amd-smi, or None."""
+    import subprocess
+    try:
+        r = subprocess.run(["amd-smi", "metric", "-p", "-c", "--json"], capture_output=True, text=True, timeout=20)
+        d = json.loads(r.stdout)["gpu_data"][0]
+        clks = [v["clk"]["value"] for k, v in d["clock"].items() if k.startswith("gfx_") and isinstance(v, dict)]
+        return float(d["power"]["socket_power"]["value"]), float(np.mean(clks))
+    except Exception:
+        return None
+
+
+def run_power(names, secs: float = 5.0) -> dict:
+    """Board power and shader clock (amd-smi, sampled several times a second) while one
+    configuration's kernel runs back to back for `secs` seconds, first on the benchmark's seeded
+    inputs, then on all-zero operands of the same shapes: the same instructions and memory traffic
+    without the data toggling.  A configuration whose time drops on zeros while the clock rises is
+    held by the chip's power management, not by its instruction schedule."""
+    import subprocess
+    import threading
+
+    import torch
+
+    import tensorvia_amd as tv
+    from tensorvia_amd.matmul import storage_to_torch as to_torch
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            t = time.time()
+            v = _smi_sample()
+            if v:
+                samples.append((t, *v))
+            time.sleep(0.05)
+
+    cap = None
+    m = re.search(r"Max Graphics Package Power \(W\):\s*([\d.]+)",
+                  subprocess.run(["rocm-smi", "--showmaxpower"], capture_output=True, text=True).stdout)
+    if m:
+        cap = float(m.group(1))
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    L = tv.lib()
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
+    out = {"cap_w": cap, "seconds": secs, "configs": {}}
+    for name in names:
+        inp = make_inputs(name)
+        dt = inp["dt"]
+        a = to_torch(inp["a"], dt)
+        b = to_torch(inp["b"], dt)
+        if name == "c4":
+            b = b.permute(0, 2, 1)
+        reps = [b] + ([b.clone() for _ in range(5)] if name.startswith("c5") else [])
+        c = tv.gemm(a, b)
+        flops, bytes_ = work(name, inp)
+        res = {}
+        for mode in ("random", "zeros"):
+            if mode == "zeros":
+                a.zero_()
+                for r_ in reps:
+                    r_.zero_()
+            descs = [tv.make_args(a, r_, c) for r_ in reps]
+            for i in range(20):
+                tv.check(L.tv_hip_gemm(ctypes.byref(descs[i % len(descs)]), sh))
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0, n = time.time(), 0
+            e0.record()
+            while time.time() - t0 < secs:
+                for i in range(50):
+                    L.tv_hip_gemm(ctypes.byref(descs[(n + i) % len(descs)]), sh)
+                n += 50
+                torch.cuda.synchronize()
+            e1.record()
+            torch.cuda.synchronize()
+            t1 = time.time()
+            ms = e0.elapsed_time(e1) / n
+            w = [(p, f) for (t, p, f) in samples if t0 + 0.7 < t < t1]
+            frac = flops / (ms * 1e-3) / 1e12 / PEAK[DTYPE[name]] if BOUND[name] == "mfma" else \
+                bytes_ / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS
+            res[mode] = {"us_per_launch": ms * 1e3, "roofline_frac": frac, "samples": len(w),
+                         "power_w_mean": float(np.mean([p for p, _ in w])) if w else None,
+                         "power_w_max": float(np.max([p for p, _ in w])) if w else None,
+                         "sclk_mhz_mean": float(np.mean([f for _, f in w])) if w else None}
+            log(f"power {name} {mode:6s}: {ms * 1e3:8.2f} us  frac {frac:.3f}  "
+                f"{res[mode]['power_w_mean'] or float('nan'):7.1f} W (max {res[mode]['power_w_max'] or float('nan'):.0f})  "
+                f"{res[mode]['sclk_mhz_mean'] or float('nan'):6.0f} MHz  ({len(w)} samples)")
+            time.sleep(1.0)
+        out["configs"][name] = res
+        del a, b, reps, c
+        torch.cuda.empty_cache()
+    stop.set()
+    th.join(timeout=30)
+    return out
+
+
 def trace_check(name: str, res: dict) -> dict | None:
     """The committed kernel trace's figures for this config's kernel, beside the live ones."""
     if not TRACE_FILE.exists() or name not in KERNEL:
@@ -492,17 +590,23 @@ def trace_summary(csv_path: str, steps: int) -> dict:
     return out
 
 
+DEFAULT_CONFIGS = "c1,c2,c3,c3_fused,bf16_4096,c4,c5m1,c5m8,cast_c3a,random_c3a,fill_c3a,transpose_c4k"
+POWER_CONFIGS = ["c2", "bf16_4096", "c3", "c1", "c4", "c5m1"]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="c1,c2,c3,c3_fused,bf16_4096,c4,c5m1,c5m8,cast_c3a,random_c3a,fill_c3a,transpose_c4k")
+    ap.add_argument("--configs", default=DEFAULT_CONFIGS)
     ap.add_argument("--only", default=None,
                     help="run only this config's GPU kernel (for profilers); 'copy' runs the traffic calibration copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--vendor", action="store_true", help="also time torch's library GEMM on the same inputs")
     ap.add_argument("--no-ops-mul", action="store_true", help="skip timing ops::Mul end to end (c1_ops_mul)")
+    ap.add_argument("--power", action="store_true",
+                    help="board power and clock (amd-smi) per GEMM config on the seeded inputs and on zeros, then exit")
     ap.add_argument("--trace-summary", metavar="CSV", default=None,
                     help="summarise a rocprofv3 kernel_trace.csv of this bench (with the same --steps) and exit")
     args = ap.parse_args()
@@ -524,6 +628,11 @@ def main() -> int:
 
     if args.only == "copy":
         print(json.dumps({"only": "copy", **run_copy(args.steps, args.warmup)}))
+        return 0
+    if args.power:
+        names = [n for n in (args.configs.split(",") if args.configs != DEFAULT_CONFIGS else POWER_CONFIGS)
+                 if n in DESC and n not in EW and n != "c3_fused"]
+        print(json.dumps({"power": run_power(names)}))
         return 0
     names = [args.only] if args.only else args.configs.split(",")
     if "c2" not in names and not args.only:
