@@ -506,7 +506,9 @@ def run_power(names, secs: float = 5.0) -> dict:
             e0.record()
             while time.time() - t0 < secs:
                 for i in range(50):
-                    L.tv_hip_gemm(ctypes.byref(descs[(n + i) % len(descs)]), sh)
+                    rc = L.tv_hip_gemm(ctypes.byref(descs[(n + i) % len(descs)]), sh)
+                    if rc:
+                        tv.check(rc)
                 n += 50
                 torch.cuda.synchronize()
             e1.record()
