@@ -29,6 +29,29 @@ constexpr F32Tile kF32Tiles[kF32TileCount] = {{128, 128, 1.0}, {64, 128, 0.96}, 
 int f32_a_mode_96(const GemmDesc& d) { return pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, 4, 96, d.pad_a); }
 int f32_b_mode(const GemmDesc& d) { return pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, 4, 128, d.pad_b); }
 
+// Compute units of the current device (cached per device; 256 if the runtime cannot tell).
+int f32_device_cus() {
+    static std::atomic<int> cached[kMaxDevices];
+    const int v = cached_per_device(cached, [](int dev) {
+        int cus = 0;
+        return hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0 ? cus : 0;
+    });
+    return v > 0 ? v : 256;
+}
+
+// A 256x256 tile (8 waves of 128x64, one workgroup per CU) reads half the operand bytes per FLOP
+// of the 128x128 tile.  It serves shapes whose 256x256 tiles fill whole rounds of the CUs with no
+// padded rows or columns: A[4096,4096] @ B[4096,4096] 979.4 against 1,003.9 us, [8192]^3 7,702
+// against 7,980 us, [4096,2048] @ [2048,4096] 499.1 against 507.2 us (same box, same process); with
+// fewer tiles than CUs the stream-K split it would need measured slower ([2048,8192] @
+// [8192,2048], 64 tiles: 533.7 against 518.4 us).
+bool f32_whole_rounds_256(const GemmDesc& d) {
+    if (d.M % 256 || d.N % 256) return false;
+    const int64_t tiles = (int64_t)(d.M / 256) * (d.N / 256) * d.batch;
+    const int cus = f32_device_cus();
+    return tiles >= cus && tiles % cus == 0;
+}
+
 int pick_f32_tile(const GemmDesc& d) {
     const int bm = f32_b_mode(d);
     const bool t96_ok = f32_a_mode_96(d) == LOAD_KCONTIG && (bm == LOAD_MNCONTIG || bm == LOAD_KCONTIG);
@@ -52,7 +75,9 @@ int pick_f32_tile(const GemmDesc& d) {
 
 int launch_gemm_mfma_f32(const GemmDesc& d, hipStream_t stream, bool may_alloc) {
     switch (pick_f32_tile(d)) {
-        case 0: return run_modes<float, 128, 128, 2, 2>(d, stream, 8, may_alloc);
+        case 0:
+            if (f32_whole_rounds_256(d)) return run_modes<float, 256, 256, 2, 4>(d, stream, 8, may_alloc);
+            return run_modes<float, 128, 128, 2, 2>(d, stream, 8, may_alloc);
         case 1: return run_modes<float, 64, 128, 2, 2>(d, stream, 8, may_alloc);
         case 2: return run_modes<float, 128, 64, 2, 2>(d, stream, 8, may_alloc);
         case 3: return run_modes<float, 32, 128, 1, 4>(d, stream, 8, may_alloc);

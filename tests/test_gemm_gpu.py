@@ -204,6 +204,45 @@ def test_fp32_96_row_tile_k_contiguous_b_exact(hip, M, K, N):
     np.testing.assert_array_equal(to_storage(plain), c)
 
 
+@pytest.mark.parametrize("batch,M,K,N,b_t,cpad", [
+    (0, 4096, 128, 4096, False, 0), (0, 4096, 100, 4096, True, 0), (2, 2048, 96, 4096, False, 0),
+    (0, 4096, 136, 4096, False, 3), (0, 8192, 40, 8192, True, 0)])
+def test_fp32_256_tile_whole_rounds_exact(hip, batch, M, K, N, b_t, cpad):
+    """fp32 shapes whose 256x256 tiles fill whole rounds of the CUs (256 or 1,024 tiles) take the
+    256x256 tile: row-major and k-contiguous B, a ragged K, a batch, and C inside wider rows (the
+    unstaged stores).  Integer-valued inputs: bit-exact against exact sums, equal to the plain
+    kernel (tv_hip_gemm_noalloc), and the fused epilogue (bias + relu) equal to the exact
+    composition."""
+    lead = (batch,) if batch else ()
+    a = ints(51, lead + (M, K), -3, 3)
+    b = ints(52, lead + (K, N), -3, 3)
+    ta = to_torch(a, FLOAT32)
+    tb = to_torch(np.ascontiguousarray(np.swapaxes(b, -1, -2)), FLOAT32).transpose(-1, -2) if b_t else to_torch(b, FLOAT32)
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
+    wide = torch.full(lead + (M, N + cpad), 9.0, dtype=torch.float32, device="cuda")
+    c = wide[..., :N]
+    hip.gemm(ta, tb, out=c)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(c.contiguous()), want)
+    if cpad:
+        assert bool((wide[..., N:] == 9.0).all())
+    plain = torch.zeros(lead + (M, N), dtype=torch.float32, device="cuda")
+    args = tv.make_args(ta, tb, plain)
+    sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    tv.check(tv.lib().tv_hip_gemm_noalloc(ctypes.byref(args), sh))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(plain), want)
+    bias = ints(53, (N,), -40, 40).astype(np.float32)
+    tbias = to_torch(bias, FLOAT32)
+    ep = tv.TvEpilogue()
+    ep.act, ep.reserved, ep.bias, ep.sbias_b, ep.sbias_m, ep.sbias_n = tv.ACT_RELU, 0, tbias.data_ptr(), 0, 0, 1
+    fused = torch.zeros(lead + (M, N), dtype=torch.float32, device="cuda")
+    args = tv.make_args(ta, tb, fused)
+    tv.check(tv.lib().tv_hip_gemm_ex(ctypes.byref(args), ctypes.byref(ep), sh))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(fused), np.maximum(want + bias, 0).astype(np.float32))
+
+
 @pytest.mark.parametrize("dt", [FLOAT32, BFLOAT16, INT8], ids=["fp32", "bf16", "int8"])
 @pytest.mark.parametrize("case", ["n1", "k1", "m1", "b1_k1_bcast", "b1_n1_at"])
 def test_unit_extent_strides(hip, dt, case):
