@@ -211,8 +211,8 @@ def test_fp32_256_tile_whole_rounds_exact(hip, batch, M, K, N, b_t, cpad):
     """fp32 shapes whose 256x256 tiles fill whole rounds of the CUs (256 or 1,024 tiles) take the
     256x256 tile: row-major and k-contiguous B, a ragged K, a batch, and C inside wider rows (the
     unstaged stores).  Integer-valued inputs: bit-exact against exact sums, equal to the plain
-    kernel (tv_hip_gemm_noalloc), and the fused epilogue (bias + relu) equal to the exact
-    composition."""
+    kernel (tv_hip_gemm_noalloc), and the fused epilogue (a column bias, then a full [M, N] bias,
+    each with relu) equal to the exact composition."""
     lead = (batch,) if batch else ()
     a = ints(51, lead + (M, K), -3, 3)
     b = ints(52, lead + (K, N), -3, 3)
@@ -241,6 +241,13 @@ def test_fp32_256_tile_whole_rounds_exact(hip, batch, M, K, N, b_t, cpad):
     tv.check(tv.lib().tv_hip_gemm_ex(ctypes.byref(args), ctypes.byref(ep), sh))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(to_storage(fused), np.maximum(want + bias, 0).astype(np.float32))
+    # a full [M, N] bias, shared by the batch (batch stride 0)
+    full = ints(54, (M, N), -40, 40).astype(np.float32)
+    tfull = to_torch(full, FLOAT32)
+    ep.bias, ep.sbias_b, ep.sbias_m, ep.sbias_n = tfull.data_ptr(), 0, N, 1
+    tv.check(tv.lib().tv_hip_gemm_ex(ctypes.byref(args), ctypes.byref(ep), sh))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_storage(fused), np.maximum(want + full, 0).astype(np.float32))
 
 
 @pytest.mark.parametrize("dt", [FLOAT32, BFLOAT16, INT8], ids=["fp32", "bf16", "int8"])
