@@ -1275,22 +1275,10 @@ static int run_smallk_cfg(const GemmDesc& d, hipStream_t stream) {
     const int tiles_n = (d.N + C::BN - 1) / C::BN;
     const int64_t nt = (int64_t)tiles_m * tiles_n * d.batch;
     if (nt > 0x7FFFFFFF) return TV_E_SHAPE;
-    int cus = 0, dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        cus = 256;
+    const int cus = device_cus();
     const int grid = (int)(nt < cus ? nt : cus);
     hipLaunchKernelGGL(gemm_smallk_kernel<C>, dim3((unsigned)grid), dim3(C::THREADS), 0, stream, d, tiles_m, tiles_n);
     return hipGetLastError();
-}
-
-// Compute units of the current device (cached per device; 256 if the runtime cannot tell).
-static int device_cus() {
-    static std::atomic<int> cached[kMaxDevices];
-    const int v = cached_per_device(cached, [](int dev) {
-        int cus = 0;
-        return hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0 ? cus : 0;
-    });
-    return v > 0 ? v : 256;
 }
 
 // The 16-bit small-K path: 128x128 tiles, groups of ceil(tiles_n / 2) persistent workgroups (one

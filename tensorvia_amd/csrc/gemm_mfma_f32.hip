@@ -29,16 +29,6 @@ constexpr F32Tile kF32Tiles[kF32TileCount] = {{128, 128, 1.0}, {64, 128, 0.96}, 
 int f32_a_mode_96(const GemmDesc& d) { return pick_mode(d.A, d.M, d.K, d.sa_m, d.sa_k, d.sa_b, d.batch, 4, 96, d.pad_a); }
 int f32_b_mode(const GemmDesc& d) { return pick_mode(d.B, d.N, d.K, d.sb_n, d.sb_k, d.sb_b, d.batch, 4, 128, d.pad_b); }
 
-// Compute units of the current device (cached per device; 256 if the runtime cannot tell).
-int f32_device_cus() {
-    static std::atomic<int> cached[kMaxDevices];
-    const int v = cached_per_device(cached, [](int dev) {
-        int cus = 0;
-        return hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0 ? cus : 0;
-    });
-    return v > 0 ? v : 256;
-}
-
 // A 256x256 tile (8 waves of 128x64, one workgroup per CU) reads half the operand bytes per FLOP
 // of the 128x128 tile.  It serves shapes whose 256x256 tiles fill whole rounds of the CUs with no
 // padded rows or columns: A[4096,4096] @ B[4096,4096] 979.4 against 1,003.9 us, [8192]^3 7,702
@@ -48,7 +38,7 @@ int f32_device_cus() {
 bool f32_whole_rounds_256(const GemmDesc& d) {
     if (d.M % 256 || d.N % 256) return false;
     const int64_t tiles = (int64_t)(d.M / 256) * (d.N / 256) * d.batch;
-    const int cus = f32_device_cus();
+    const int cus = device_cus();
     return tiles >= cus && tiles % cus == 0;
 }
 

@@ -222,6 +222,16 @@ template <class F> inline int cached_per_device(std::atomic<int> (&slot)[kMaxDev
     return v;
 }
 
+// Compute units of the current device (cached per device; 256 if the runtime cannot tell).
+inline int device_cus() {
+    static std::atomic<int> cached[kMaxDevices];
+    const int v = cached_per_device(cached, [](int dev) {
+        int cus = 0;
+        return hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0 ? cus : 0;
+    });
+    return v > 0 ? v : 256;
+}
+
 // Buffer loads: a lane offset at or above 2^31 is outside every buffer resource built by make_rsrc
 // (num_records <= 2^30), also after a stride multiple below 2^30 is added to it, and such a load
 // returns zeros.
