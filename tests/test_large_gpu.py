@@ -285,3 +285,24 @@ def test_cpp_api_past_4gib(hip):
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
     assert "ok round_trip 4294979641 bytes" in r.stdout, r.stdout
     assert "ok mul int8 [131072,40960]@[40960,256]: 12 sampled rows" in r.stdout, r.stdout
+
+
+@pytest.mark.parametrize("dt,batch,M,K,N,bcast", [
+    (torch.bfloat16, 100003, 40, 40, 48, False), (torch.bfloat16, 100003, 3, 64, 64, False),
+    (torch.float16, 20003, 128, 32, 128, False), (torch.float32, 100003, 17, 33, 19, False),
+    (torch.int8, 100003, 24, 64, 40, True), (torch.int16, 30011, 5, 7, 9, False)],
+    ids=["bf16_gemm", "bf16_gemv", "fp16_small_k", "fp32", "int8_bcast_b", "int16_simt"])
+def test_many_small_batches(hip, dt, batch, M, K, N, bcast):
+    """Tens of thousands of small matrices in one call (the batch folds into the grid's first
+    dimension): every route (the direct-load GEMM, the GEMV, the small-K kernel, fp32 tiles, a B
+    broadcast over the batch, the SIMT kernel) exact against numpy's sums of the integer inputs."""
+    a = _ints((batch, M, K), -3, 3, dt if dt != torch.int16 else torch.int8, 111).to(dt)
+    b = _ints((K, N) if bcast else (batch, K, N), -3, 3, dt if dt != torch.int16 else torch.int8, 112).to(dt)
+    c = hip.gemm(a, b)
+    torch.cuda.synchronize()
+    want = np.matmul(a.cpu().to(torch.float64).numpy(), b.cpu().to(torch.float64).numpy())
+    got = c.cpu()
+    if dt in (torch.int8, torch.int16):
+        np.testing.assert_array_equal(got.numpy(), want.astype(np.int64).astype(got.numpy().dtype))
+    else:
+        np.testing.assert_array_equal(got.to(torch.float64).numpy(), torch.from_numpy(want).to(dt).to(torch.float64).numpy())
