@@ -204,19 +204,20 @@ def test_fp32_96_row_tile_k_contiguous_b_exact(hip, M, K, N):
     np.testing.assert_array_equal(to_storage(plain), c)
 
 
-@pytest.mark.parametrize("batch,M,K,N,b_t,cpad", [
-    (0, 4096, 128, 4096, False, 0), (0, 4096, 100, 4096, True, 0), (2, 2048, 96, 4096, False, 0),
-    (0, 4096, 136, 4096, False, 3), (0, 8192, 40, 8192, True, 0)])
-def test_fp32_256_tile_whole_rounds_exact(hip, batch, M, K, N, b_t, cpad):
+@pytest.mark.parametrize("batch,M,K,N,a_t,b_t,cpad", [
+    (0, 4096, 128, 4096, False, False, 0), (0, 4096, 100, 4096, False, True, 0), (2, 2048, 96, 4096, False, False, 0),
+    (0, 4096, 136, 4096, False, False, 3), (0, 8192, 40, 8192, False, True, 0), (0, 4096, 64, 4096, True, False, 0),
+    (2, 4096, 72, 2048, True, True, 0)])
+def test_fp32_256_tile_whole_rounds_exact(hip, batch, M, K, N, a_t, b_t, cpad):
     """fp32 shapes whose 256x256 tiles fill whole rounds of the CUs (256 or 1,024 tiles) take the
-    256x256 tile: row-major and k-contiguous B, a ragged K, a batch, and C inside wider rows (the
-    unstaged stores).  Integer-valued inputs: bit-exact against exact sums, equal to the plain
+    256x256 tile: row-major and transposed A and B, a ragged K, batches, and C inside wider rows
+    (the unstaged stores).  Integer-valued inputs: bit-exact against exact sums, equal to the plain
     kernel (tv_hip_gemm_noalloc), and the fused epilogue (a column bias, then a full [M, N] bias,
     each with relu) equal to the exact composition."""
     lead = (batch,) if batch else ()
     a = ints(51, lead + (M, K), -3, 3)
     b = ints(52, lead + (K, N), -3, 3)
-    ta = to_torch(a, FLOAT32)
+    ta = to_torch(np.ascontiguousarray(np.swapaxes(a, -1, -2)), FLOAT32).transpose(-1, -2) if a_t else to_torch(a, FLOAT32)
     tb = to_torch(np.ascontiguousarray(np.swapaxes(b, -1, -2)), FLOAT32).transpose(-1, -2) if b_t else to_torch(b, FLOAT32)
     want = np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
     wide = torch.full(lead + (M, N + cpad), 9.0, dtype=torch.float32, device="cuda")
