@@ -607,6 +607,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--vendor", action="store_true", help="also time torch's library GEMM on the same inputs")
     ap.add_argument("--no-ops-mul", action="store_true", help="skip timing ops::Mul end to end (c1_ops_mul)")
+    ap.add_argument("--no-power", action="store_true",
+                    help="skip the short c2 power/clock sample (seeded inputs, then zeros) of the default run")
     ap.add_argument("--power", action="store_true",
                     help="board power and clock (amd-smi) per GEMM config on the seeded inputs and on zeros, then exit")
     ap.add_argument("--trace-summary", metavar="CSV", default=None,
@@ -680,6 +682,11 @@ def main() -> int:
             log(f"ops::Mul c1: {c['cached']['ops_mul_ms']:.3f} ms per call with the block cache, "
                 f"{c.get('uncached', {}).get('ops_mul_ms', float('nan')):.3f} ms without")
 
+    power = None
+    if not args.no_power:
+        log("power and clock during c2 (amd-smi): seeded inputs, then zeroed operands")
+        power = run_power(["c2"], secs=2.0)
+
     head = results["c2"]
     traffic = None
     tf = ROOT / "profiles" / "gemm_int8_c2_traffic.json"
@@ -722,6 +729,10 @@ def main() -> int:
             "value", "unit", "cores", "kind", "sample", "nproc", "omp_num_threads", "openmp_threads", "effective_threads")},
         "configs": results,
     }
+    if power is not None:
+        line["power"] = {**power, "note": "board power (W) and gfx clock (MHz) sampled while c2 runs back to back; "
+                                          "the same kernel on zeroed operands shows what the clock the power cap "
+                                          "allows costs (profiles/power_clock_random_vs_zero.md)"}
     print(json.dumps(line))
     return 0
 
