@@ -471,10 +471,12 @@ def run_power(names, secs: float = 5.0) -> dict:
             time.sleep(0.05)
 
     cap = None
-    m = re.search(r"Max Graphics Package Power \(W\):\s*([\d.]+)",
-                  subprocess.run(["rocm-smi", "--showmaxpower"], capture_output=True, text=True).stdout)
-    if m:
-        cap = float(m.group(1))
+    try:
+        m = re.search(r"Max Graphics Package Power \(W\):\s*([\d.]+)",
+                      subprocess.run(["rocm-smi", "--showmaxpower"], capture_output=True, text=True, timeout=20).stdout)
+        cap = float(m.group(1)) if m else None
+    except (OSError, subprocess.SubprocessError):
+        pass
     th = threading.Thread(target=sampler, daemon=True)
     th.start()
     L = tv.lib()
