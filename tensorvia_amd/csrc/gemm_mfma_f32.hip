@@ -32,7 +32,8 @@ int f32_b_mode(const GemmDesc& d) { return pick_mode(d.B, d.N, d.K, d.sb_n, d.sb
 // A 256x256 tile (8 waves of 128x64, one workgroup per CU) reads half the operand bytes per FLOP
 // of the 128x128 tile.  It serves shapes whose 256x256 tiles fill whole rounds of the CUs with no
 // padded rows or columns: A[4096,4096] @ B[4096,4096] 979.4 against 1,003.9 us, [8192]^3 7,702
-// against 7,980 us, [4096,2048] @ [2048,4096] 499.1 against 507.2 us (same box, same process); with
+// against 7,980 us, [4096,2048] @ [2048,4096] 499.1 against 507.2 us (same box, same process; both
+// on the persistent stream-K kernel, before whole rounds took the plain kernel); with
 // fewer tiles than CUs the stream-K split it would need measured slower ([2048,8192] @
 // [8192,2048], 64 tiles: 533.7 against 518.4 us).
 bool f32_whole_rounds_256(const GemmDesc& d) {

@@ -861,11 +861,15 @@ static int sk_grid() {
 }
 
 // The stream-K launch: K of at least 32 k-tiles (8 when the tiles do not fill the CUs), at least 8
-// k-tiles per workgroup.  Measured against one workgroup per tile with random fp32 inputs (same
-// box, settled clocks): c1 [2592,2048]@[2048,4096] 349 against 380 us; 768 tiles 411 against
-// 432 us; 1024 tiles (K 1024-4096) 5-6 % faster; [1024]^3 (64 tiles) 37.9 against 68.0 us; but
-// 363 tiles at K = 512 (16 k-tiles) 78.7 against 75.0 us, the combines outweighing the balance.
-// Returns 1 if it did not launch.
+// k-tiles per workgroup, and a last round that the resident workgroups do not fill.  Measured
+// against one workgroup per tile with random fp32 inputs (same box, settled clocks): c1
+// [2592,2048]@[2048,4096] 349 against 380 us; 768 tiles 411 against 432 us; [1024]^3 (64 tiles)
+// 37.9 against 68.0 us; but 363 tiles at K = 512 (16 k-tiles) 78.7 against 75.0 us, the combines
+// outweighing the balance.  Tile counts of whole rounds run one workgroup per tile, which measured
+// faster than this kernel's persistent loop over them and needs no slots: [4096]^3 on 256x256
+// tiles 948.3 against 972.6 us, [8192]^3 7,534 against 7,649, [8][1024,1024]@[1024,1024] (512
+// tiles of 128x128) 130.1 against 132.6, [16][128,4096]@[4096,8192] (1,024 tiles) 995.6 against
+// 998.8.  Returns 1 if it did not launch.
 template <class C, bool FUSED>
 static int run_cfg_sk(const GemmDesc& d, hipStream_t stream, int group_m, int tiles_m, int tiles_n, int64_t ntiles, int c_vec) {
     const int nk = (d.K + C::BK - 1) / C::BK;
@@ -873,6 +877,7 @@ static int run_cfg_sk(const GemmDesc& d, hipStream_t stream, int group_m, int ti
     int G = sk_grid<C>();
     if (G <= 0) return 1;
     if (nk < 32 && ntiles >= G / 2) return 1; // G / 2: about one tile per CU
+    if (ntiles % G == 0) return 1;            // whole rounds: nothing to split
     // Whole rounds of G tiles run whole; only the last, partial round is split.
     const int64_t dp = ntiles > G ? ntiles / G * G : 0;
     const int64_t iters = (ntiles - dp) * nk;
