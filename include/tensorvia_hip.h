@@ -38,7 +38,11 @@
  * Semantics (matching the reference CPU backend, src/backend/cpu/mul.cpp:97-145):
  *   C[b, m, n] = sum_k A[b, m, k] * B[b, k, n]
  *   - element (b, m, k) of A lives at  A + b*sa_b + m*sa_m + k*sa_k  (element units);
- *     sa_b == 0 broadcasts A over the batch, likewise sb_b for B;
+ *     sa_b == 0 broadcasts A over the batch, likewise sb_b for B (and a zero row or k stride
+ *     repeats a row or column); the stride of a dimension of extent 1 is ignored;
+ *   - strides along extents above 1 must not be negative, C's must not be zero (no two outputs in
+ *     one element), and each operand's elements must lie within 2^56 bytes of its first element;
+ *     other descriptors return TV_E_SHAPE;
  *   - int8 x int8: exact int32 accumulation; dtype_c INT8 stores the low byte of the exact sum
  *     (the reference's wrap-around result), dtype_c INT32 stores the full sum;
  *   - bf16/fp16 inputs: fp32 accumulation, output bf16/fp16 (GPU-backend convention) or FLOAT32
@@ -81,7 +85,8 @@ enum tv_dtype {
 enum tv_status {
     TV_OK = 0,
     TV_E_NULL = -1,        /* a required pointer is NULL */
-    TV_E_SHAPE = -2,       /* batch/M/N/K negative or above TV_MAX_EXTENT, or a size overflows the kernels' index range */
+    TV_E_SHAPE = -2,       /* batch/M/N/K negative or above TV_MAX_EXTENT, a size overflows the kernels' index range, or a
+                              stride is not allowed (see the semantics above) */
     TV_E_DTYPE = -3,       /* dtype value out of range or output dtype not allowed for the inputs */
     TV_E_UNSUPPORTED = -4, /* valid request that this entry point does not serve (e.g. gemv with M > 8) */
     TV_E_INJECTED = -5,    /* returned by the fault-injection hook (tests only) */
@@ -90,8 +95,8 @@ enum tv_status {
 };
 
 /* Largest batch, M, N or K the GEMM entry points accept: 2^31 - 2^20 - 1.  Tile, k-tile and slice
- * counts are 32-bit; the margin keeps their rounded-up sums in range.  Operands, outputs and their
- * strides may span any number of bytes: every address is formed in 64 bits. */
+ * counts are 32-bit; the margin keeps their rounded-up sums in range.  Operands and outputs may
+ * span up to 2^56 bytes: every address is formed in 64 bits. */
 #define TV_MAX_EXTENT 2146435071
 
 typedef struct tv_gemm_args {

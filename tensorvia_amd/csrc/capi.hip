@@ -58,6 +58,23 @@ bool mfma_pair(const tv_gemm_args* a) {
     }
 }
 
+// Bytes from a strided operand's first element to its last: (extent - 1) * stride summed over its
+// three dimensions, times the element size.  A dimension of extent 0 or 1 never steps, so its
+// stride counts nothing.  -1 when a stride along an extent above 1 is negative.
+__int128 span_bytes(const int64_t (&ext)[3], const int64_t (&str)[3], size_t es) {
+    __int128 span = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (ext[i] <= 1) continue;
+        if (str[i] < 0) return -1;
+        span += (__int128)(ext[i] - 1) * str[i];
+    }
+    return span * (__int128)es;
+}
+
+// Largest span accepted: 2^56 bytes, above any device's memory, so that every address a kernel
+// forms (base + offsets, in 64 bits) stays in range.
+constexpr __int128 kMaxSpan = (__int128)1 << 56;
+
 int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
     if (!a) return TV_E_NULL;
     if (a->flags != 0) return TV_E_UNSUPPORTED;
@@ -72,6 +89,15 @@ int validate(const tv_gemm_args* a, tvk::GemmDesc* d) {
     if (!mfma_pair(a) && a->dtype_c != cpu_result_type(a->dtype_a, a->dtype_b)) return TV_E_DTYPE;
     const bool empty = a->batch == 0 || a->M == 0 || a->N == 0;
     if (!empty) {
+        // Strides along extents above 1: not negative (the loaders and stores add 32-bit offsets
+        // to a row's or tile's base), and C's not zero either (two outputs in one element).  A and
+        // B are not read when K = 0.
+        const __int128 sa = span_bytes({a->batch, a->M, a->K}, {a->sa_b, a->sa_m, a->sa_k}, tvk::dtype_size(a->dtype_a));
+        const __int128 sb = span_bytes({a->batch, a->K, a->N}, {a->sb_b, a->sb_k, a->sb_n}, tvk::dtype_size(a->dtype_b));
+        const __int128 sc = span_bytes({a->batch, a->M, a->N}, {a->sc_b, a->sc_m, a->sc_n}, tvk::dtype_size(a->dtype_c));
+        if ((a->K > 0 && (sa < 0 || sa >= kMaxSpan || sb < 0 || sb >= kMaxSpan)) || sc < 0 || sc >= kMaxSpan)
+            return TV_E_SHAPE;
+        if ((a->batch > 1 && a->sc_b == 0) || (a->M > 1 && a->sc_m == 0) || (a->N > 1 && a->sc_n == 0)) return TV_E_SHAPE;
         if (!a->C) return TV_E_NULL;
         if (a->K > 0 && (!a->A || !a->B)) return TV_E_NULL;
     }
@@ -162,10 +188,10 @@ int tv_hip_gemm_ex(const tv_gemm_args* args, const tv_epilogue* ep, void* hip_st
             if (ep->sbias_b < 0 || ep->sbias_m < 0 || ep->sbias_n < 0) return TV_E_SHAPE;
             // Extent of the elements read, in bytes: every offset stays below 2^30 (one buffer
             // resource, 32-bit offsets).
-            const int64_t last = (d.batch - 1 > 0 ? (int64_t)(d.batch - 1) : 0) * ep->sbias_b +
-                                 (d.M > 0 ? d.M - 1 : 0) * ep->sbias_m + (d.N > 0 ? d.N - 1 : 0) * ep->sbias_n;
-            const int64_t bytes = (last + 1) * (int64_t)tvk::dtype_size(args->dtype_c);
-            if (last > ((int64_t)1 << 30) || bytes > ((int64_t)1 << 30)) return TV_E_UNSUPPORTED;
+            const size_t es = tvk::dtype_size(args->dtype_c);
+            const __int128 span = span_bytes({d.batch, d.M, d.N}, {ep->sbias_b, ep->sbias_m, ep->sbias_n}, es);
+            if (span + (__int128)es > ((__int128)1 << 30)) return TV_E_UNSUPPORTED;
+            const int64_t bytes = (int64_t)span + (int64_t)es;
             d.bias = ep->bias;
             d.sbias_b = ep->sbias_b;
             d.sbias_m = ep->sbias_m;
@@ -196,12 +222,13 @@ int tv_hip_repack(const tv_repack_args* args, void* hip_stream) {
     if (!args) return TV_E_NULL;
     if (args->ndim < 0 || args->ndim > TV_MAX_DIMS) return TV_E_SHAPE;
     if (args->elem_size != 1 && args->elem_size != 2 && args->elem_size != 4 && args->elem_size != 8) return TV_E_DTYPE;
-    int64_t n = 1;
-    for (int d = 0; d < args->ndim; ++d) {
+    for (int d = 0; d < args->ndim; ++d)
         if (args->shape[d] < 0) return TV_E_SHAPE;
-        n *= args->shape[d];
-    }
-    if (n == 0) return TV_OK;
+    for (int d = 0; d < args->ndim; ++d)
+        if (args->shape[d] == 0) return TV_OK; // empty view
+    int64_t n = 1; // element count: must fit in 64 bits
+    for (int d = 0; d < args->ndim; ++d)
+        if (__builtin_mul_overflow(n, args->shape[d], &n)) return TV_E_SHAPE;
     if (!args->src || !args->dst) return TV_E_NULL;
     return tvk::launch_repack(args, static_cast<hipStream_t>(hip_stream));
 }

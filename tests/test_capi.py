@@ -63,7 +63,7 @@ def _args(**kw):
     a.dtype_a = a.dtype_b = a.dtype_c = tv.FLOAT32
     a.batch, a.M, a.N, a.K = 1, 4, 4, 4
     a.A, a.B, a.C = 16, 32, 48  # never dereferenced: every case below returns before a launch
-    a.sa_m, a.sa_k, a.sb_k, a.sb_n, a.sc_m, a.sc_n = 4, 1, 4, 1, 4, 1
+    a.sa_m, a.sa_k, a.sb_k, a.sb_n, a.sc_b, a.sc_m, a.sc_n = 4, 1, 4, 1, 16, 4, 1
     for k, v in kw.items():
         setattr(a, k, v)
     return a
@@ -93,6 +93,58 @@ def test_rejections(fn):
     # empty problems are valid no-ops
     assert _call(fn, _args(M=0, A=None, B=None, C=None)) == tv.TV_OK
     assert _call(fn, _args(batch=0)) == tv.TV_OK
+
+
+@pytest.mark.parametrize("fn", ["tv_hip_gemm", "tv_hip_gemv", "tv_hip_gemm_noalloc"])
+def test_stride_rejections(fn):
+    """Negative strides along extents above 1, zero strides of C there, and operands spanning 2^56
+    bytes or more are rejected before any launch; the same strides on an extent of 1 are ignored.
+    Calls whose strides pass stop at the missing output pointer (checked after the strides)."""
+    for f in ("sa_m", "sa_k", "sb_k", "sb_n", "sc_m", "sc_n"):
+        assert _call(fn, _args(**{f: -4})) == tv.TV_E_SHAPE, f
+    assert _call(fn, _args(batch=2, sa_b=-16)) == tv.TV_E_SHAPE
+    assert _call(fn, _args(batch=2, sb_b=-16)) == tv.TV_E_SHAPE
+    assert _call(fn, _args(batch=2, sc_b=-16, sa_b=16)) == tv.TV_E_SHAPE
+    for f in ("sc_m", "sc_n"):
+        assert _call(fn, _args(**{f: 0})) == tv.TV_E_SHAPE, f  # two outputs in one element
+    assert _call(fn, _args(batch=2, sc_b=0)) == tv.TV_E_SHAPE
+    # zero strides of A and B broadcast: accepted
+    assert _call(fn, _args(batch=2, sa_b=0, sb_b=0, sa_m=0, sb_k=0, C=None)) == tv.TV_E_NULL
+    # extent 1: the stride is ignored, whatever its value
+    assert _call(fn, _args(M=1, sa_m=-(1 << 62), sc_m=0, C=None)) == tv.TV_E_NULL
+    assert _call(fn, _args(sa_b=-(1 << 62), sb_b=1 << 62, sc_b=-5, C=None)) == tv.TV_E_NULL  # batch 1
+    # K = 0 reads neither operand: their strides are not checked
+    assert _call(fn, _args(K=0, sa_m=-4, sb_n=-1, C=None)) == tv.TV_E_NULL
+    # span: (M - 1) * sa_m * 4 bytes against 2^56, also where the product overflows 64 bits
+    assert _call(fn, _args(sa_m=(1 << 54) // 3 - 1, C=None)) == tv.TV_E_NULL
+    assert _call(fn, _args(sa_m=(1 << 54) // 3 + 1)) == tv.TV_E_SHAPE
+    assert _call(fn, _args(sc_n=1 << 61)) == tv.TV_E_SHAPE
+    assert _call(fn, _args(batch=3, sb_b=(1 << 63) - 1)) == tv.TV_E_SHAPE
+
+
+def test_repack_rejections():
+    """tv_hip_repack rejects bad ranks, element sizes and shapes, and shapes whose element count
+    overflows 64 bits, before any launch; a view with a zero extent is an empty no-op wherever the
+    zero stands."""
+    L = tv.lib()
+
+    def call(shape, elem_size=2, src=64, dst=128):
+        a = tv.TvRepackArgs()
+        a.ndim, a.elem_size, a.src, a.dst = len(shape), elem_size, src, dst
+        for i, n in enumerate(shape):
+            a.shape[i], a.strides[i] = n, 1
+        return L.tv_hip_repack(ctypes.byref(a), None)
+
+    assert L.tv_hip_repack(None, None) == tv.TV_E_NULL
+    assert call([2, 2], elem_size=3) == tv.TV_E_DTYPE
+    assert call([2, -1]) == tv.TV_E_SHAPE
+    assert call([1 << 40, 1 << 40]) == tv.TV_E_SHAPE  # 2^80 elements
+    assert call([1 << 40, 1 << 40, 0], src=None, dst=None) == tv.TV_OK
+    assert call([0, 1 << 40, 1 << 40], src=None, dst=None) == tv.TV_OK
+    assert call([4, 4], src=None) == tv.TV_E_NULL
+    a = tv.TvRepackArgs()
+    a.ndim = tv.TV_MAX_DIMS + 1
+    assert L.tv_hip_repack(ctypes.byref(a), None) == tv.TV_E_SHAPE
 
 
 def test_elementwise_rejections():
@@ -140,6 +192,12 @@ def test_gemm_ex_rejections():
     assert call(_args(dtype_a=tv.INT32, dtype_b=tv.INT32, dtype_c=tv.INT32), act=tv.ACT_RELU) == tv.TV_E_UNSUPPORTED
     assert call(_args(dtype_c=-1), act=tv.ACT_RELU) == tv.TV_E_DTYPE
     assert call(_args(M=0, A=None, B=None, C=None), act=tv.ACT_SILU) == tv.TV_OK
+    # bias strides: negative ones are rejected, and the elements read must lie within 2^30 bytes
+    # (one buffer resource), also where (M - 1) * stride overflows 64 bits
+    assert call(_args(), act=tv.ACT_RELU, bias=64, sbias_m=-1) == tv.TV_E_SHAPE
+    assert call(_args(), act=tv.ACT_RELU, bias=64, sbias_n=1 << 28) == tv.TV_E_UNSUPPORTED
+    assert call(_args(), act=tv.ACT_RELU, bias=64, sbias_m=1 << 62) == tv.TV_E_UNSUPPORTED
+    assert call(_args(batch=3), act=tv.ACT_RELU, bias=64, sbias_b=(1 << 63) - 1) == tv.TV_E_UNSUPPORTED
     L.tv_hip_inject_fault(tv.TV_E_INJECTED, 1)
     assert call(_args(), act=tv.ACT_RELU) == tv.TV_E_INJECTED
     L.tv_hip_inject_fault(0, 0)
