@@ -656,7 +656,7 @@ __device__ inline void write_tile_fixed(const Acc (&acc)[C::FM][C::FN], char* ld
     constexpr int PITCH = ROWB + 16;
     constexpr int RPP = staged_rows<C::WM, PITCH, WAVE_BYTES>();
     constexpr int CPR = ROWB / 16;
-    static_assert(RPP >= 16 && C::WM % RPP == 0 && RPP * PITCH <= WAVE_BYTES && (RPP * CPR) % 64 == 0,
+    static_assert(RPP % 16 == 0 && C::WM % RPP == 0 && RPP * PITCH <= WAVE_BYTES && (RPP * CPR) % 64 == 0,
                   "staging pass must be whole wave stores");
     typedef TC vec_t __attribute__((__vector_size__(4 * sizeof(TC))));
 #pragma unroll

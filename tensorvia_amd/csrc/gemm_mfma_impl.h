@@ -315,12 +315,13 @@ constexpr int kEpiWaveBytes = 18432;
 // in 16-byte row chunks, so every global store covers whole row segments.  Rows are processed in
 // passes of RPP (all WM rows for 1- and 2-byte outputs).  Requires a contiguous row (sc_n == 1)
 // with 16-byte aligned row starts at the tile's column origin.
-// Rows per staging pass: the largest of WM, WM/2, WM/4, ... (a multiple of 16) whose padded rows
-// fit in the wave's staging bytes.
+// Rows per staging pass: the largest multiple of 16 that divides WM (a pass takes whole 16-row
+// fragment blocks) and whose padded rows fit in the wave's staging bytes; 16 when none does, which
+// the callers' static_asserts then reject.  (Halving WM instead would give 24 rows for WM = 48.)
 template <int WM, int PITCH, int WAVE_BYTES> constexpr int staged_rows() {
-    int r = WM;
-    while (r > 16 && r * PITCH > WAVE_BYTES) r /= 2;
-    return r;
+    for (int r = WM - WM % 16; r > 16; r -= 16)
+        if (WM % r == 0 && r * PITCH <= WAVE_BYTES) return r;
+    return 16;
 }
 
 // Value transform of the staged store: identity for a plain matmul.
@@ -335,7 +336,7 @@ __device__ inline void write_tile_staged(const Acc (&acc)[C::FM][C::FN], char* l
     constexpr int PITCH = ROWB + 16;
     constexpr int RPP = staged_rows<C::WM, PITCH, WAVE_BYTES>(); // rows per pass
     constexpr int CPR = ROWB / 16;                            // 16-byte chunks per row
-    static_assert(RPP >= 16 && C::WM % RPP == 0 && RPP * PITCH <= WAVE_BYTES, "staging area too small");
+    static_assert(RPP % 16 == 0 && C::WM % RPP == 0 && RPP * PITCH <= WAVE_BYTES, "staging area too small");
     typedef TC vec_t __attribute__((__vector_size__(4 * sizeof(TC))));
 #pragma unroll
     for (int pass = 0; pass < C::WM / RPP; ++pass) {
@@ -393,7 +394,7 @@ __device__ inline void write_tile_staged_epi(const f32x4 (&acc)[C::FM][C::FN], c
     constexpr int PITCH = ROWB + 16;
     constexpr int RPP = staged_rows<C::WM, PITCH, WAVE_BYTES>();
     constexpr int CPR = ROWB / 16; // 4-column float chunks per row
-    static_assert(RPP >= 16 && C::WM % RPP == 0 && RPP * PITCH <= WAVE_BYTES, "staging area too small");
+    static_assert(RPP % 16 == 0 && C::WM % RPP == 0 && RPP * PITCH <= WAVE_BYTES, "staging area too small");
     typedef TC out4 __attribute__((__vector_size__(4 * sizeof(TC))));
     const bool has_bias = d.bias != nullptr;
     const __amdgpu_buffer_rsrc_t br = make_rsrc(static_cast<const char*>(d.bias), has_bias ? d.bias_bytes : 0);
