@@ -608,8 +608,7 @@ void gemm_dma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c
                 for (int i = 0; i < C::FM; ++i)
 #pragma unroll
                     for (int j = 0; j < C::FN; ++j)
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[i][j]), r,
-                                                               (((wave * C::FM + i) * C::FN + j) * 64 + lane) * 16, 0, 16);
+                        slot_store16(r, (((wave * C::FM + i) * C::FN + j) * 64 + lane) * 16, acc[i][j]);
             }
             publish_and_count(sk.cnt + tile, last - first + 1, &last_flag);
             if (!last_flag) continue;
@@ -619,8 +618,7 @@ void gemm_dma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c
                 for (int i = 0; i < C::FM; ++i) {
 #pragma unroll
                     for (int j = 0; j < C::FN; ++j) {
-                        const Acc p = __builtin_bit_cast(
-                            Acc, __builtin_amdgcn_raw_buffer_load_b128(r, (((wave * C::FM + i) * C::FN + j) * 64 + lane) * 16, 0, 16));
+                        const Acc p = slot_load16<Acc>(r, (((wave * C::FM + i) * C::FN + j) * 64 + lane) * 16);
                         acc[i][j] = v == first ? p : acc[i][j] + p;
                     }
                     // one row of slot loads at a time: with all of them hoisted, the loads and the
@@ -628,7 +626,7 @@ void gemm_dma_sk_kernel(GemmDesc d, int tiles_m, int tiles_n, int group_m, int c
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            if (threadIdx.x == 0) __hip_atomic_store(sk.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            slot_count_reset(sk.cnt + tile);
         }
         dma_tile_store<C, FUSED>(d, L, b, m0, n0, c_vec, acc);
     }

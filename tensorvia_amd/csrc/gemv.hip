@@ -284,7 +284,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
     if (part == 0)
 #pragma unroll
         for (int m = 0; m < MR; ++m)
-            if (m < d.M) __hip_atomic_store(slots + ((int64_t)s * MR + m) * NB + oc, v[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (m < d.M) slot_store(slots + ((int64_t)s * MR + m) * NB + oc, v[m]);
     publish_and_count(g.cnt + strip, g.nslices, &last_flag);
     if (!last_flag) return;
     for (int o = tid; o < MR * NB; o += THREADS) {
@@ -294,9 +294,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
             Acc part_v[kGemvMaxSlices];
 #pragma unroll
             for (int k = 0; k < kGemvMaxSlices; ++k)
-                part_v[k] = k < g.nslices ? __hip_atomic_load(slots + ((int64_t)k * MR + m) * NB + c, __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT)
-                                          : Acc(0);
+                part_v[k] = k < g.nslices ? slot_load(slots + ((int64_t)k * MR + m) * NB + c) : Acc(0);
             Acc t = part_v[0];
 #pragma unroll
             for (int k = 1; k < kGemvMaxSlices; ++k)
@@ -304,7 +302,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvArgs g) {
             gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + c) * d.sc_n, d.dtype_c, gemv_epilogue(t, d, b, m, n0 + c));
         }
     }
-    if (tid == 0) __hip_atomic_store(g.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    slot_count_reset(g.cnt + strip);
 }
 
 // Matrix-core variant for 16-bit and int8 W (the dot-product loop above is VALU-bound at larger M:
@@ -505,7 +503,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
 #pragma unroll
     for (int i = 0; i < OPT; ++i)
         if ((tid + THREADS * i) / NB < d.M)
-            __hip_atomic_store(slots + (int64_t)s * XR * NB + tid + THREADS * i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            slot_store(slots + (int64_t)s * XR * NB + tid + THREADS * i, v[i]);
     publish_and_count(g.cnt + strip, g.nslices, &last_flag);
     if (!last_flag) return;
 #pragma unroll
@@ -515,8 +513,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
             Acc part_v[kGemvMaxSlices];
 #pragma unroll
             for (int k = 0; k < kGemvMaxSlices; ++k)
-                part_v[k] = k < g.nslices ? __hip_atomic_load(slots + (int64_t)k * XR * NB + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                          : Acc(0);
+                part_v[k] = k < g.nslices ? slot_load(slots + (int64_t)k * XR * NB + o) : Acc(0);
             Acc t = part_v[0];
 #pragma unroll
             for (int k = 1; k < kGemvMaxSlices; ++k)
@@ -524,7 +521,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs g) {
             gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)(n0 + c) * d.sc_n, d.dtype_c, gemv_epilogue(t, d, b, m, n0 + c));
         }
     }
-    if (tid == 0) __hip_atomic_store(g.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    slot_count_reset(g.cnt + strip);
 }
 
 
@@ -649,7 +646,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kt_kernel(GemvArgs g) {
         for (int r = 0; r < 4; ++r) {
             const int m = 16 * mb + 4 * kg + r;
             if (m < d.M && m < XR)
-                __hip_atomic_store(slots + ((int64_t)s * XR + m) * NB + col, acc[mb][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                slot_store(slots + ((int64_t)s * XR + m) * NB + col, acc[mb][r]);
         }
     publish_and_count(g.cnt + strip, g.nslices, &last_flag);
     if (!last_flag) return;
@@ -663,9 +660,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kt_kernel(GemvArgs g) {
                     Acc part_v[kGemvMaxSlices];
 #pragma unroll
                     for (int k = 0; k < kGemvMaxSlices; ++k)
-                        part_v[k] = k < g.nslices ? __hip_atomic_load(slots + ((int64_t)k * XR + m) * NB + col, __ATOMIC_RELAXED,
-                                                                      __HIP_MEMORY_SCOPE_AGENT)
-                                                  : Acc(0);
+                        part_v[k] = k < g.nslices ? slot_load(slots + ((int64_t)k * XR + m) * NB + col) : Acc(0);
                     Acc t = part_v[0];
 #pragma unroll
                     for (int k = 1; k < kGemvMaxSlices; ++k)
@@ -673,7 +668,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kt_kernel(GemvArgs g) {
                     gemv_store(Cb, (int64_t)m * d.sc_m + (int64_t)n * d.sc_n, d.dtype_c, gemv_epilogue(t, d, b, m, n));
                 }
             }
-    if (tid == 0) __hip_atomic_store(g.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    slot_count_reset(g.cnt + strip);
 }
 
 __global__ __launch_bounds__(256) void gemv_zero_kernel(int* p, int64_t n) {

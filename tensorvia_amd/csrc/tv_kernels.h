@@ -125,12 +125,33 @@ __device__ inline float epilogue_value(float v, const GemmDesc& d, int64_t b, in
 // also writes back and invalidates the XCD's whole L2 (buffer_wbl2 sc1, buffer_inv sc1) once per
 // wave, which measured 104 us on c5 (x[1,4096] @ W[4096,11008] bf16) against 18.5 us with this
 // hand-over; there is no dirty non-atomic data here for those to write back.
-// *last is 1 in the workgroup that must combine the slots.
+// *last is 1 in the workgroup that must combine the slots.  Every slot access and the count's reset
+// go through the slot_* helpers below, which carry that policy.
 __device__ inline void publish_and_count(int* cnt, int nslices, int* last) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) *last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nslices - 1;
     __syncthreads();
+}
+
+// Partial-slot stores and loads of the hand-over above: scalar slots as agent-scope relaxed
+// atomics, 16-byte slots through a buffer resource with the sc1 cache-policy bit (16).
+constexpr int kSlotPolicy = 16;
+template <typename T> __device__ inline void slot_store(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T> __device__ inline T slot_load(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename V> __device__ inline void slot_store16(__amdgpu_buffer_rsrc_t r, int off, V v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, off, 0, kSlotPolicy);
+}
+template <typename V> __device__ inline V slot_load16(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSlotPolicy));
+}
+// The combining workgroup leaves the block's count at zero for the next launch.
+__device__ inline void slot_count_reset(int* cnt) {
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Operand load modes for one GEMM operand (A: rows m, B: rows n; "K-contiguous" means the
