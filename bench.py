@@ -560,8 +560,10 @@ def trace_summary(csv_path: str, steps: int) -> dict:
     """Per-configuration durations (End - Start) of the last `steps` dispatches of each
     configuration's kernel in a rocprofv3 kernel_trace.csv of `bench.py --steps S --no-cpu`: the
     timed launches close each configuration's run of back-to-back dispatches.  A kernel's dispatches
-    are cut into runs at gaps of more than 2 ms; configurations that share a kernel (c5 M=1, then
-    M=8) take its runs in order, the others its longest run."""
+    are cut into runs at gaps of more than 2 ms, and runs shorter than `steps` dropped; configurations
+    that share a kernel (c5 M=1, then M=8) take its runs in order, the others its first run (a
+    later run of the same kernel, such as the c2 power sample's zeroed operands at the end of the
+    default run, is not the configuration's timing)."""
     import csv
     import re
     import statistics as st
@@ -584,7 +586,7 @@ def trace_summary(csv_path: str, steps: int) -> dict:
         if pat in used:
             i = used[pat] + 1
         else:
-            i = 0 if name == "c5m1" else max(range(len(runs)), key=lambda j: len(runs[j]))
+            i = 0
         if i >= len(runs):
             continue
         used[pat] = i
