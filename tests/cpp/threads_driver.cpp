@@ -1,8 +1,8 @@
 // GPU driver for the C++ API used from several host threads at once.  The HIP context is shared:
 // one stream, the block cache and the pinned staging chunks, each behind its own mutex.  Four
-// threads each run 12 rounds of ops::Random -> ops::Mul -> to_host() on their own operands
-// (int8, bf16, fp32 and int8 again, different shapes); every round must give the same bytes as
-// the thread's first round, and the int8 threads' sampled rows must equal the low byte of the exact
+// threads each run 12 iterations of ops::Random -> ops::Mul -> to_host() on their own operands
+// (int8, bf16, fp32 and int8 again, different shapes); every iteration must give the same bytes as
+// the thread's first iteration, and the int8 threads' sampled rows must equal the low byte of the exact
 // sums.  Prints "ok thread <t> ..." or "mismatch thread <t> ..." lines; exit status 1 on any failure.
 #include <cstdint>
 #include <cstdio>
@@ -34,12 +34,12 @@ std::vector<uint8_t> bytes_of(Tensor t) {
 
 bool run(int t, const Job& j) {
     std::vector<uint8_t> first;
-    for (int round = 0; round < 12; ++round) {
+    for (int it = 0; it < 12; ++it) {
         Tensor a = ops::Random({j.M, j.K}, j.dt, -10, 10, j.seed);
         Tensor b = ops::Random({j.K, j.N}, j.dt, -10, 10, j.seed + 1);
         Tensor c = ops::Mul(a, b);
         std::vector<uint8_t> got = bytes_of(c);
-        if (round == 0) {
+        if (it == 0) {
             first = got;
             if (j.dt == DataType::INT8) {
                 const std::vector<uint8_t> A = bytes_of(a), B = bytes_of(b);
@@ -57,12 +57,12 @@ bool run(int t, const Job& j) {
             }
         } else if (got != first) {
             std::lock_guard<std::mutex> lk(g_print);
-            std::printf("mismatch thread %d: round %d differs from round 0\n", t, round);
+            std::printf("mismatch thread %d: iteration %d differs from iteration 0\n", t, it);
             return false;
         }
     }
     std::lock_guard<std::mutex> lk(g_print);
-    std::printf("ok thread %d: 12 rounds of [%ld,%ld]@[%ld,%ld] dtype %d\n", t, long(j.M), long(j.K), long(j.K), long(j.N),
+    std::printf("ok thread %d: 12 iterations of [%ld,%ld]@[%ld,%ld] dtype %d\n", t, long(j.M), long(j.K), long(j.K), long(j.N),
                 static_cast<int>(j.dt));
     return true;
 }

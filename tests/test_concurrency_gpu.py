@@ -83,11 +83,11 @@ def test_threads_on_separate_streams_exact(hip):
 
 
 def test_cpp_api_from_four_threads(hip):
-    """Four threads share the C++ API's HIP context, 12 rounds each (int8, bf16, fp32 GEMV, int8
-    GEMV): every round's bytes equal the thread's first round, and the int8 threads' sampled rows
+    """Four threads share the C++ API's HIP context, 12 iterations each (int8, bf16, fp32 GEMV, int8
+    GEMV): every iteration's bytes equal the thread's first, and the int8 threads' sampled rows
     equal the low byte of the exact sums (tests/cpp/threads_driver.cpp, in a child process)."""
     from tests.cpp import build as cpp
     r = subprocess.run([str(cpp.binary("threads_driver"))], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
     for t in range(4):
-        assert f"ok thread {t}: 12 rounds" in r.stdout, r.stdout
+        assert f"ok thread {t}: 12 iterations" in r.stdout, r.stdout
