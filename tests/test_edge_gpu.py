@@ -3,7 +3,9 @@
 * K = 0: every output is the empty sum (through the fused epilogue: act(bias)), on the GEMV-shaped
   and GEMM-shaped routes of tv_hip_gemm, tv_hip_gemv and tv_hip_gemm_ex;
 * the GEMV kernels at the LDS cap on x's K-slice: shapes whose strip count leaves one K-slice per
-  strip, so each slice is as long as x's LDS rows allow (8,192 int8 rows, 4,096 bf16 rows).
+  strip, so each slice is as long as x's LDS rows allow (8,192 int8 rows, 4,096 bf16 rows);
+* descriptors the C-ABI refuses (zero output strides, negative strides, 2^56-byte spans) on real
+  device buffers: refused before any launch, C untouched.
 
 The reference's mul_kernel_basic (src/backend/cpu/mul.cpp:7-25) sums nothing for K = 0 and stores
 the zero it started from; for the cap cases the bars are the usual ones (int8 bit-exact against the
@@ -109,3 +111,31 @@ def test_gemv_int8_dot_product_at_lds_cap(hip):
     tx, tw = to_torch(x, INT8), to_torch(w, INT8)
     np.testing.assert_array_equal(to_storage(hip.gemv(tx, tw, out_dtype=INT32)), exact.astype(np.int32))
     np.testing.assert_array_equal(to_storage(hip.gemv(tx, tw)), exact.astype(np.int8))
+
+
+@pytest.mark.parametrize("entry", ["gemm", "gemv", "noalloc"])
+def test_refused_descriptors_leave_c_untouched(hip, entry):
+    """Descriptors the C-ABI refuses (a row-expanded output, i.e. two outputs in one element; a
+    negative row stride of A; an operand spanning 2^56 bytes) return TV_E_SHAPE before any launch:
+    C, filled with a sentinel, is unchanged after the stream has drained.  Real device buffers, so
+    a launch that slipped through would write C."""
+    M, K, N = 4, 64, 64
+    a = to_torch(rng.uniform_int(1, M * K, -3, 3).reshape(M, K).astype(np.float32), FLOAT32)
+    b = to_torch(rng.uniform_int(2, K * N, -3, 3).reshape(K, N).astype(np.float32), FLOAT32)
+    c = torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    fn = {"gemm": tv.lib().tv_hip_gemm, "gemv": tv.lib().tv_hip_gemv, "noalloc": tv.lib().tv_hip_gemm_noalloc}[entry]
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    good = tv.make_args(a, b, c)
+    for field, value in (("sc_m", 0), ("sa_m", -K), ("sb_k", 1 << 55)):
+        args = tv.make_args(a, b, c)
+        setattr(args, field, value)
+        if field == "sa_m":
+            args.A = a.data_ptr() + (M - 1) * K * 4  # last row first, stepping back: in bounds
+        assert fn(ctypes.byref(args), s) == tv.TV_E_SHAPE, field
+    torch.cuda.synchronize()
+    assert torch.equal(c, torch.full_like(c, 7.0))
+    # the unmodified descriptor runs
+    assert fn(ctypes.byref(good), s) == tv.TV_OK
+    torch.cuda.synchronize()
+    want = rng.uniform_int(1, M * K, -3, 3).reshape(M, K).astype(np.float64) @ rng.uniform_int(2, K * N, -3, 3).reshape(K, N)
+    np.testing.assert_array_equal(to_storage(c).astype(np.float64), want)
